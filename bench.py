@@ -1,0 +1,183 @@
+"""Motion-decoder throughput on one MI355X: frames/s at 512x512, f16 weights.
+
+A step decodes one batch of 16 frames (the 250-frame throughput workload is
+decoded in launches of 16; consecutive steps walk its AR(1) latent sequence)
+with every input resident in HBM: latents in device memory, frames written
+to device memory.  Prints ONE JSON line (see the keys below).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 16]
+                    [--ftype f16|f32] [--workload iid|smooth|stress]
+                    [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "talking-portrait.cpp_amd")
+sys.path[:0] = [ROOT, PKG]
+
+PEAK_HBM_GBS = 8000.0
+PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}
+REF_FPS_RTX5070TI = 213.2   # mdec, GGML-CUDA f16 fast graph (docs/vulkan-perf.md:134,143)
+
+
+def stage_costs(ic, oc, nframes, ftype):
+    """algorithmic FLOPs and HBM bytes of every profiled launch group of one
+    decode_batch call (slot order of tpmd_stage_times)"""
+    sa = 2 if ftype == "f16" else 4   # conv operand / activation bytes
+    sw = sa                            # conv weight bytes
+    C0 = ic[0]
+    # style GEMV + demod + conv1: latents, modulation weights, conv1 weights
+    # and its output; FLOPs of conv1 only
+    f0 = 2 * nframes * 16 * 9 * C0 * C0
+    b0 = nframes * 512 * 4 + 9 * C0 * C0 * sw + nframes * 16 * C0 * sa
+    slots = [("style+conv1", f0, b0)]
+    for j in range(len(ic)):
+        r = 8 << j
+        IC, OC = ic[j], oc[j]
+        last = j + 1 == len(ic)
+        f_up = 2 * nframes * r * r * 9 * IC * OC
+        b_up = nframes * (r // 2) ** 2 * IC * sa + nframes * r * r * OC * sa + 4 * OC * 9 * IC * sw
+        f_dn = 2 * nframes * r * r * 9 * OC * OC
+        b_dn = nframes * r * r * OC * sa + nframes * r * r * OC * 4 + 9 * OC * OC * sw
+        # tail: read out (f32) + feats once + prev skips; write trunk, flow, rgb
+        b_tl = (nframes * r * r * OC * 4 + r * r * OC * sa
+                + (nframes * 2 * 3 * (r // 2) ** 2 * 4 if j else 0)
+                + (0 if last else nframes * r * r * OC * sa + nframes * 3 * r * r * 4)
+                + nframes * 3 * r * r * 4)
+        f_tl = nframes * r * r * OC * 2 * 6
+        slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv", f_dn, b_dn), (f"r{r}.tail", f_tl, b_tl)]
+    return slots
+
+
+def roofline(name, flops, nbytes, us, ftype):
+    ridge = PEAK_TFLOPS[ftype] * 1e12 / (PEAK_HBM_GBS * 1e9)
+    ai = flops / max(nbytes, 1)
+    if ai >= ridge and flops > 0:
+        ach = flops / (us * 1e-6) / 1e12
+        return {"name": name, "us": round(us, 2), "bound": "mfma", "achieved": round(ach, 2),
+                "peak": PEAK_TFLOPS[ftype], "unit": "TFLOP/s", "frac": round(ach / PEAK_TFLOPS[ftype], 4)}
+    ach = nbytes / (us * 1e-6) / 1e9
+    return {"name": name, "us": round(us, 2), "bound": "hbm", "achieved": round(ach, 1),
+            "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4)}
+
+
+def cpu_baseline(ftype_unused=None):
+    """the CPU oracle's fast graph (f32, numpy/OpenBLAS + OpenMP C ops) on
+    this host, one 512x512 frame"""
+    from oracle import mdec as om
+    import synth
+    threads = len(os.sched_getaffinity(0))
+    om.set_threads(threads)
+    raw, lat, feats = synth.workload("iid", 2, "f32")
+    dec = om.Decoder(raw, "f32")
+    dec.set_feats(feats)
+    dec.decode_fast(lat[:1])          # warm-up (page-in, BLAS init)
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        dec.decode_fast(lat[n % 2: n % 2 + 1])
+        n += 1
+        if time.perf_counter() - t0 > 10.0 or n >= 8:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 4), "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{n} frame(s) of the f32 fast-graph oracle at 512x512, i.i.d. workload"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--ftype", default="f16", choices=["f16", "f32"])
+    ap.add_argument("--workload", default="iid", choices=["iid", "smooth", "stress"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(frames shard across GPUs with no per-frame collective; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import synth
+    import tpmd
+
+    B = args.batch
+    n_seq = 250
+    raw, lat, feats = synth.workload(args.workload, n_seq, args.ftype)
+    dec = tpmd.MotionDecoder(args.ftype, 7, device=0)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(B)
+    dec.set_feats(feats)
+    lat_dev = torch.from_numpy(np.concatenate([lat, lat[:B]])).cuda()   # wrap-around window
+    imgs = torch.empty((B, 3, 512, 512), dtype=torch.float32, device="cuda")
+
+    def step(k):
+        t0 = (k * B) % n_seq
+        dec.decode_batch_device(lat_dev[t0:t0 + B], imgs)
+
+    for k in range(args.warmup):
+        step(k)
+    dec.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(k)
+    dec.sync()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    fps = args.steps * B / dt
+
+    # per-stage durations: HIP events recorded by the library on its stream
+    nslot = dec.profile_stages(True)
+    acc = np.zeros(nslot)
+    nprof = max(5, min(args.steps, 20))
+    for k in range(nprof):
+        step(k)
+        acc += np.array(dec.stage_times())
+    dec.profile_stages(False)
+    us = acc / nprof
+    slots = stage_costs(dec.ic, dec.oc, B, args.ftype)
+    stages = [roofline(n, f, b, u, args.ftype) for (n, f, b), u in zip(slots, us)]
+    dom = max(range(len(stages)), key=lambda i: stages[i]["us"])
+    r = dict(stages[dom])
+    r["kernel"] = r.pop("name")
+    r["traffic"] = None
+    r.pop("us")
+
+    out = {
+        "metric": "motion-decoder frames/sec @512x512 f16, 1 GPU",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(fps / REF_FPS_RTX5070TI, 3) if args.ftype == "f16" else None,
+        "dtype": "f16" if args.ftype == "f16" else "f32",
+        "data": "synthetic",
+        "config": {"workload": f"LIA motion decoder 512x512, {n_seq}-frame AR(1) latent sequence "
+                               f"({args.workload} inputs), {B} frames per launch chain",
+                   "frames_per_step": B, "resolution": 512, "ftype": args.ftype,
+                   "stage_channels_in": list(dec.ic), "stage_channels_out": list(dec.oc)},
+        "roofline": r,
+        "stages": stages,
+        "stage_sum_us": round(float(us.sum()), 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/* tpmd.h — C ABI of the MI355X (gfx950) motion decoder of talking-portrait.cpp.
+ *
+ * This library replaces the per-frame LIA/StyleGAN motion decoder of the
+ * reference (`tp::motion_dec`, src/motion_dec.h:10-49, src/motion_dec.cpp)
+ * with hand-written HIP kernels.  Everything above the decoder (tp.h,
+ * pipeline, encoders) is unchanged: the reference's motion_dec methods map
+ * one-to-one onto the entry points below (see the citations), and the C++
+ * shim in talking-portrait.cpp_amd/host/motion_dec.h keeps their exact
+ * names and signatures.
+ *
+ * Conventions (the reference's tp.h contract, include/tp.h:3-10): opaque
+ * handle, caller-owned flat buffers, fixed-width types, no exceptions cross
+ * this boundary.  Functions returning int return 0 on success and -1 on
+ * failure; the reason is then available from tpmd_last_error(ctx).  Every
+ * destroy is NULL-safe.  A context is used by one thread at a time.
+ *
+ * Layouts (ggml "ne" order in the reference, fastest first):
+ *   style / latent : [frame][512] f32
+ *   image          : [frame][3][R][R] f32, CHW (the reference's img chunks)
+ *   feats j        : [r_j*r_j][OC_j] f32, pixel-major channel-fastest
+ *                    (menc_result.feats, src/motion_enc.h:12-19)
+ *   CL map         : [frame][y][x][channel]  (the fast graph's [C, N, B])
+ *   SP map         : [frame][channel][y][x]  (the spatial [W, H, C, B])
+ */
+#ifndef TPMD_H
+#define TPMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TPMD_ABI_VERSION 1
+#define TPMD_MAX_STAGES 7
+#define TPMD_STYLE_DIM 512
+
+typedef struct tpmd_ctx tpmd_ctx;
+
+/* tp_abi_version (include/tp.h:27) — the decoder library's own ABI level. */
+int tpmd_abi_version(void);
+
+/* Create a decoder on HIP device `device`.
+ * Replaces backend_t::init + motion_dec construction (src/backend.cpp:9-57,
+ * src/tp.cpp:13-41).  ftype "f32" | "f16" follows tp_load's ftype
+ * (include/tp.h:33-35, src/tp.cpp:17-30): f16 keeps the big file-f16
+ * weights in f16 (f16-in / f32-accumulate MFMA), f32 computes in f32.
+ * n_stages: 1..7 pyramid stages (7 = full 512x512 decoder; fewer truncates
+ * like TP_MDEC_STAGES, src/motion_dec.cpp:787-792).  stage_ic / stage_oc:
+ * NULL for the reference channels {512,512,512,512,256,128,64} /
+ * {512,512,512,256,128,64,32} (src/motion_dec.cpp:12-13), or per-stage lists
+ * (multiples of 32, stage_ic[j+1] == stage_oc[j]) for reduced test models.
+ * Returns NULL on failure (message on stderr). */
+tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *stage_ic,
+                      const int *stage_oc);
+void tpmd_destroy(tpmd_ctx *ctx);
+/* tp_last_error (include/tp.h:38) */
+const char *tpmd_last_error(const tpmd_ctx *ctx);
+
+/* weight flags */
+#define TPMD_W_F16_FILE 1 /* tensor is stored f16 in the GGUF (gtype 1) */
+#define TPMD_W_FOLDED 2   /* data already carries motion_ae_scale folding */
+
+/* Hand one decoder tensor to the library, by its GGUF name and torch layout
+ * (e.g. "dec.convs.3.conv.weight", [1,OC,IC,3,3] row-major), as f32 host
+ * data.  Replaces weights_t::load for the dec.* tensors
+ * (src/gguf_load.cpp:146-194): unless TPMD_W_FOLDED, the load-time scale
+ * folding of motion_ae_scale (src/motion_enc.cpp:14-45) is applied here;
+ * with ftype f16, tensors flagged TPMD_W_F16_FILE with >= 4096 elements are
+ * stored f16 (src/gguf_load.cpp:149-153).  n = element count (checked). */
+int tpmd_set_weight(tpmd_ctx *ctx, const char *name, const float *data, int64_t n, int flags);
+
+/* motion_dec::prepare (src/motion_dec.h:38, src/motion_dec.cpp:31-226):
+ * S_aug demodulation Gram rows, composed sub-pixel up-conv kernels, cf GEMM
+ * matrices; uploads every derived tensor.  Fails naming the first missing
+ * tensor ("missing tensor <name>"). */
+int tpmd_prepare(tpmd_ctx *ctx);
+
+/* motion_dec::build (src/motion_dec.h:41, src/motion_dec.cpp:659-1135):
+ * allocate the persistent per-batch buffers for up to max_batch frames per
+ * call (1..256) and the stage constants.  Requires tpmd_prepare. */
+int tpmd_build(tpmd_ctx *ctx, int max_batch);
+/* frames per call chosen at build (motion_dec::batch, src/motion_dec.h:28) */
+int tpmd_batch(const tpmd_ctx *ctx);
+/* output resolution R = 8 << (n_stages - 1) */
+int tpmd_out_res(const tpmd_ctx *ctx);
+
+/* motion_dec::set_feats (src/motion_dec.h:43, src/motion_dec.cpp:1137-1160):
+ * feats[j] = [r_j*r_j][OC_j] f32 host, j < n_stages; stored f16 in f16
+ * mode.  Requires tpmd_build ("decoder not built"). */
+int tpmd_set_feats(tpmd_ctx *ctx, const float *const *feats);
+/* same from device memory (f32) */
+int tpmd_set_feats_device(tpmd_ctx *ctx, const float *const *feats_dev);
+
+/* motion_dec::decode_batch (src/motion_dec.h:46-47,
+ * src/motion_dec.cpp:1190-1220): n (1..batch) latents -> n frames.
+ * styles: [n][512]; imgs: [n][3][R][R]; both host pointers
+ * (on_device = 0, synchronous like the reference) or device pointers
+ * (on_device = 1; enqueued on the decoder's stream, see tpmd_sync). */
+int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, int on_device);
+/* motion_dec::decode (src/motion_dec.h:44-45, :1162-1188): one frame. */
+int tpmd_decode(tpmd_ctx *ctx, const float *style, float *img);
+/* wait for work enqueued by on_device calls */
+int tpmd_sync(tpmd_ctx *ctx);
+
+/* Per-stage timing of the next decode_batch: when enabled, the call records
+ * HIP events around each launch group and stores microseconds into
+ * us[0..n_slots) (slot 0 = style + demod + conv1, then 3 per stage: up-conv,
+ * dense conv, tail).  Returns the slot count, or -1. */
+int tpmd_profile_stages(tpmd_ctx *ctx, int enable);
+int tpmd_stage_times(const tpmd_ctx *ctx, float *us, int max_slots);
+
+/* ---- per-stage entry points on DEVICE buffers (f32 in / f32 out) -------
+ * These run one piece of the decoder with the context's weights, for
+ * parity tests and per-stage measurement.  `stream` is a hipStream_t
+ * (NULL = the context stream); they are asynchronous on it. */
+
+/* ModulatedConv2d with demodulation + FusedLeakyReLU (styled_conv /
+ * styled_conv_up / styled_conv_input, src/motion_dec.cpp:357-433):
+ * conv = 0 for dec.conv1, 1 + i for dec.convs.i (even i: 2x sub-pixel
+ * up-conv).  x: CL [n][H][W][IC]; s: [n][IC] style of this conv (the
+ * demodulation is computed from it); y: CL [n][H'][W'][OC]. */
+int tpmd_modconv(tpmd_ctx *ctx, int conv, const float *x, int n, int H, int W, const float *s,
+                 float *y, void *stream);
+
+/* Stage tail of stage j (src/motion_dec.cpp:1077-1108): ToFlow (+ flow
+ * skip), flow head, grid_sample warp of feats j, warp/trunk blend, ToRGB
+ * (+ rgb skip).  out: CL [n][r][r][C] dense-conv output; s_flow: [n][C];
+ * flow_prev / rgb_prev: SP [n][3][r/2][r/2] or NULL (stage 0); outputs
+ * flow: SP [n][3][r][r] (or NULL), trunk: CL f32 (or NULL), rgb: SP,
+ * warp: CL f32 (or NULL). */
+int tpmd_stage_tail(tpmd_ctx *ctx, int j, const float *out, int n, const float *s_flow,
+                    const float *flow_prev, const float *rgb_prev, float *flow, float *trunk,
+                    float *rgb, float *warp, void *stream);
+
+/* ---- op-level entry points (no context) ------------------------------- */
+
+/* GGML_OP_BILINEAR_GATHER (patches/ggml-tp-ops.patch:41-60, :104-111,
+ * CUDA :688-752): torch grid_sample, bilinear, zeros padding,
+ * align_corners=False.  feat: [W*H][C] channel-fastest, f32 (feat_f16 = 0)
+ * or IEEE f16 (feat_f16 = 1); grid: interleaved [N][2] (planar = 0, the
+ * ggml [2, N]) or planar [2][N] (planar = 1, ggml_bilinear_gather_planar);
+ * dst: [N][C] (sp = 0) or [C][N] (sp = 1, ggml_bilinear_gather_sp).
+ * Device pointers; returns 0 or -1 (invalid arguments). */
+int tpmd_gather(const void *feat, int feat_f16, int C, int W, int H, const float *grid, int64_t N,
+                int planar, int sp, float *dst, void *stream);
+/* the gather's integer tap selection and weights: x0 = floor(fx),
+ * y0 = floor(fy), wx = fx - x0, wy = fy - y0 per point (device pointers) */
+int tpmd_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0,
+                     int32_t *y0, float *wx, float *wy, void *stream);
+/* GGML_OP_UPFIRDN2X (patch :128-134, :996-1045): SP [CB][H][W] -> [CB][2H][2W] */
+int tpmd_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB,
+                   void *stream);
+/* GGML_OP_FLOW_GRID (patch :94-102, :1082-1104): fl [3][N], xs [2][N] -> [3][N] */
+int tpmd_flow_grid(const float *fl, const float *xs, float *y, int64_t N, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TPMD_H */

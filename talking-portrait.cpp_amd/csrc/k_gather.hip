@@ -1,0 +1,214 @@
+// Bilinear grid-sample gather and the small per-pixel ops of the decoder's
+// stage tail, as standalone kernels (the op-level surface of
+// patches/ggml-tp-ops.patch: GGML_OP_BILINEAR_GATHER :683-752,
+// GGML_OP_UPFIRDN2X :996-1045, GGML_OP_FLOW_GRID :1082-1104).
+//
+// The decoder itself runs these inside the fused stage-tail kernel
+// (k_tail.hip); the standalone forms serve the op-level C ABI and tests.
+#include "tpmd_device.h"
+#include "tpmd_launch.h"
+
+namespace tpmd {
+
+// ---------------------------------------------------------------------------
+// CL gather, vectorised: G lanes share one grid point and split its C
+// channels in 16-byte chunks (CPL chunks per lane, C = G * CPL * VEC).  All
+// lanes of a group read the same tap rows, so a wave reads whole contiguous
+// channel runs of the feature map (coalesced) and writes a contiguous
+// [C] output row per point.
+template <typename TF, int G, int CPL>
+__global__ __launch_bounds__(256) void gather_cl_vec(const TF *__restrict__ feat,
+                                                     const float *__restrict__ grid,
+                                                     float *__restrict__ dst, int C, int W, int H,
+                                                     int64_t N, int planar) {
+#pragma clang fp contract(off)
+    constexpr int VEC = vec16<TF>::n;
+    typedef typename vec16<TF>::type vt;
+    constexpr int PPW = 64 / G;  // points per wave
+    const int lane = threadIdx.x & 63;
+    const int gl = lane % G, grp = lane / G;
+    const int64_t wave = (int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t) gridDim.x * (blockDim.x >> 6);
+    for (int64_t n = wave * PPW + grp; n < N; n += nwaves * PPW) {
+        const float gx = planar ? grid[n] : grid[2 * n];
+        const float gy = planar ? grid[N + n] : grid[2 * n + 1];
+        const taps4 t = gather_geometry(gx, gy, W, H);
+        float acc[CPL][VEC];
+#pragma unroll
+        for (int ch = 0; ch < CPL; ch++)
+#pragma unroll
+            for (int e = 0; e < VEC; e++) acc[ch][e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
+            if (cx < 0 || cx >= W || cy < 0 || cy >= H) continue;
+            const float w = tap_weight(t, k);
+            const TF *f = feat + (int64_t) (cy * W + cx) * C;
+#pragma unroll
+            for (int ch = 0; ch < CPL; ch++) {
+                const vt v = *(const vt *) (f + (ch * G + gl) * VEC);
+#pragma unroll
+                for (int e = 0; e < VEC; e++) acc[ch][e] += w * to_f32(v[e]);
+            }
+        }
+        float *d = dst + n * C;
+#pragma unroll
+        for (int ch = 0; ch < CPL; ch++) {
+            float *dd = d + (ch * G + gl) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; e += 4)
+                *(floatx4 *) (dd + e) = floatx4{acc[ch][e], acc[ch][e + 1], acc[ch][e + 2], acc[ch][e + 3]};
+        }
+    }
+}
+
+// one thread per output element (any C, CL or SP output): the layout- and
+// size-generic form, mirroring the reference kernel's indexing
+template <typename TF>
+__global__ __launch_bounds__(256) void gather_elem(const TF *__restrict__ feat,
+                                                   const float *__restrict__ grid,
+                                                   float *__restrict__ dst, int C, int W, int H,
+                                                   int64_t N, int planar, int sp) {
+#pragma clang fp contract(off)
+    const int64_t total = (int64_t) C * N;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        const int c = sp ? (int) (i / N) : (int) (i % C);
+        const int64_t n = sp ? i % N : i / C;
+        const float gx = planar ? grid[n] : grid[2 * n];
+        const float gy = planar ? grid[N + n] : grid[2 * n + 1];
+        const taps4 t = gather_geometry(gx, gy, W, H);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
+            if (cx < 0 || cx >= W || cy < 0 || cy >= H) continue;
+            acc += tap_weight(t, k) * to_f32(feat[(int64_t) (cy * W + cx) * C + c]);
+        }
+        dst[i] = acc;
+    }
+}
+
+// integer tap selection and f32 weights per point
+__global__ __launch_bounds__(256) void gather_taps_kernel(const float *__restrict__ grid, int W,
+                                                          int H, int64_t N, int planar,
+                                                          int32_t *__restrict__ x0,
+                                                          int32_t *__restrict__ y0,
+                                                          float *__restrict__ wx,
+                                                          float *__restrict__ wy) {
+    for (int64_t n = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; n < N;
+         n += (int64_t) gridDim.x * blockDim.x) {
+        const float gx = planar ? grid[n] : grid[2 * n];
+        const float gy = planar ? grid[N + n] : grid[2 * n + 1];
+        const taps4 t = gather_geometry(gx, gy, W, H);
+        x0[n] = t.x0;
+        y0[n] = t.y0;
+        wx[n] = t.wx;
+        wy[n] = t.wy;
+    }
+}
+
+// upfirdn2d(up=2, pad=(2,1)): SP [CB][H][W] -> [CB][2H][2W]
+__global__ __launch_bounds__(256) void upfirdn2x_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ k4,
+                                                        float *__restrict__ y, int W, int H,
+                                                        int64_t CB) {
+    const int64_t total = 4 * (int64_t) W * H * CB;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        const int X = (int) (i % (2 * W));
+        const int Y = (int) ((i / (2 * W)) % (2 * H));
+        const int64_t cb = i / (4 * (int64_t) W * H);
+        y[i] = upfirdn2x_at(x + (int64_t) W * H * cb, W, H, k4, X, Y);
+    }
+}
+
+// flow head: fl SP [3][N], xs planar [2][N] -> [3][N] (gx, gy, mask)
+__global__ __launch_bounds__(256) void flow_grid_kernel(const float *__restrict__ fl,
+                                                        const float *__restrict__ xs,
+                                                        float *__restrict__ y, int64_t N) {
+#pragma clang fp contract(off)
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < 3 * N;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t pln = i / N, n = i % N;
+        y[i] = pln == 2 ? 1.0f / (1.0f + expf(-fl[2 * N + n])) : tanhf(fl[pln * N + n]) + xs[pln * N + n];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+
+static int grid_for(int64_t work, int per_block) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > 65536) g = 65536;
+    return (int) g;
+}
+
+template <typename TF>
+static hipError_t launch_gather_typed(const TF *feat, const float *grid, float *dst, int C, int W,
+                                      int H, int64_t N, int planar, int sp, hipStream_t st) {
+    constexpr int VEC = vec16<TF>::n;
+    const bool aligned = (((uintptr_t) feat | (uintptr_t) dst) & 15) == 0;
+    if (!sp && C % VEC == 0 && aligned) {
+        const int lpp = C / VEC;
+        int G = 0, CPL = 0;
+        if (lpp <= 64 && (lpp & (lpp - 1)) == 0) {
+            G = lpp;
+            CPL = 1;
+        } else if (lpp % 64 == 0 && (lpp / 64 == 2 || lpp / 64 == 4)) {
+            G = 64;
+            CPL = lpp / 64;
+        }
+        if (G) {
+            const int ppb = 4 * (64 / G);  // points per 256-thread block
+            const int nb = grid_for(N, ppb);
+#define TPMD_G(g, cpl)                                                                        \
+    if (G == g && CPL == cpl) {                                                               \
+        hipLaunchKernelGGL((gather_cl_vec<TF, g, cpl>), dim3(nb), dim3(256), 0, st, feat, grid, \
+                           dst, C, W, H, N, planar);                                          \
+        return hipGetLastError();                                                             \
+    }
+            TPMD_G(1, 1) TPMD_G(2, 1) TPMD_G(4, 1) TPMD_G(8, 1) TPMD_G(16, 1) TPMD_G(32, 1)
+            TPMD_G(64, 1) TPMD_G(64, 2) TPMD_G(64, 4)
+#undef TPMD_G
+        }
+    }
+    hipLaunchKernelGGL((gather_elem<TF>), dim3(grid_for((int64_t) C * N, 256)), dim3(256), 0, st,
+                       feat, grid, dst, C, W, H, N, planar, sp);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const void *feat, bool feat_f16, const float *grid, float *dst, int C,
+                         int W, int H, int64_t N, int planar, int sp, hipStream_t st) {
+    if (N <= 0 || C <= 0) return hipSuccess;
+    if (feat_f16)
+        return launch_gather_typed((const half_t *) feat, grid, dst, C, W, H, N, planar, sp, st);
+    return launch_gather_typed((const float *) feat, grid, dst, C, W, H, N, planar, sp, st);
+}
+
+hipError_t launch_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0,
+                              int32_t *y0, float *wx, float *wy, hipStream_t st) {
+    if (N <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_taps_kernel, dim3(grid_for(N, 256)), dim3(256), 0, st, grid, W, H,
+                       N, planar, x0, y0, wx, wy);
+    return hipGetLastError();
+}
+
+hipError_t launch_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB,
+                            hipStream_t st) {
+    if (CB <= 0 || W <= 0 || H <= 0) return hipSuccess;
+    hipLaunchKernelGGL(upfirdn2x_kernel, dim3(grid_for(4 * (int64_t) W * H * CB, 256)), dim3(256),
+                       0, st, x, k4, y, W, H, CB);
+    return hipGetLastError();
+}
+
+hipError_t launch_flow_grid(const float *fl, const float *xs, float *y, int64_t N,
+                            hipStream_t st) {
+    if (N <= 0) return hipSuccess;
+    hipLaunchKernelGGL(flow_grid_kernel, dim3(grid_for(3 * N, 256)), dim3(256), 0, st, fl, xs, y,
+                       N);
+    return hipGetLastError();
+}
+
+}  // namespace tpmd

@@ -1,0 +1,868 @@
+// Host side of the MI355X motion decoder: the C ABI of include/tpmd.h.
+//
+// Mirrors the reference's motion_dec lifecycle (src/motion_dec.h:34-47):
+//   set_weight* -> prepare -> build -> set_feats -> decode_batch ...
+// prepare() restates src/motion_dec.cpp:31-226 (S_aug, composed sub-pixel
+// kernels, cf GEMM matrices) and the load-time folding of
+// src/motion_enc.cpp:14-45 / src/gguf_load.cpp:146-194; decode_batch()
+// enqueues the whole batched decoder on one HIP stream:
+//   style GEMV, demod, conv1 input, conv1,
+//   then per stage j: sub-pixel up-conv, dense conv, fused tail.
+#include "tpmd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "tpmd_launch.h"
+
+using namespace tpmd;
+
+namespace {
+
+const int REF_IC[7] = {512, 512, 512, 512, 256, 128, 64};
+const int REF_OC[7] = {512, 512, 512, 256, 128, 64, 32};
+
+struct HostTensor {
+    std::vector<float> data;  // scale-folded f32
+    int flags = 0;
+};
+
+struct ConvW {
+    int ic = 0, oc = 0;
+    bool up = false;
+    void *A = nullptr;         // act [M][9*IC], M = oc or 4*oc
+    float *bias = nullptr;     // [oc] activate.bias (x sqrt2)
+    int64_t saug_off = 0;      // into saug_all, [oc][ic+1]
+    int seg = 0;               // style segment
+    int64_t s_off = 0, d_off = 0;  // [batch][ic] / [batch][oc] blocks (set at build)
+};
+
+struct StageW {
+    float *wflow = nullptr, *fbias = nullptr, *fup = nullptr;
+    float *wrgb = nullptr, *rlb = nullptr, *rbias = nullptr, *rup = nullptr;
+    float *lin = nullptr;
+    void *feat = nullptr;      // act [r*r][oc]
+    int seg = 0;
+    int64_t s_off = 0;
+};
+
+std::string fmt(const char *f, ...) __attribute__((format(printf, 1, 2)));
+std::string fmt(const char *f, ...) {
+    char b[512];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(b, sizeof b, f, ap);
+    va_end(ap);
+    return b;
+}
+
+float round_f16(float v) { return (float) (_Float16) v; }
+
+}  // namespace
+
+struct tpmd_ctx {
+    int device = 0;
+    bool f16 = false;
+    int ns = 7;
+    int ic[7] = {}, oc[7] = {};
+    std::string err;
+    hipStream_t stream = nullptr;
+
+    std::map<std::string, HostTensor> host;
+    bool prepared = false, built = false, feats_set = false;
+    std::vector<void *> allocs;      // weights / constants
+    std::vector<void *> batch_allocs;
+
+    ConvW conv[15];
+    StageW st[7];
+    int nconv = 0;
+    float *wmod = nullptr, *bmod = nullptr;  // [R][512], [R]
+    int seg_width[kMaxSeg] = {};
+    int nseg = 0, R_total = 0;
+    float *input_cl = nullptr;        // [16][C0]
+    float *saug_all = nullptr;
+    SegTable seg{};
+    DemodTable dem{};
+
+    int batch = 0;
+    float *lat = nullptr, *s_all = nullptr, *den_all = nullptr;
+    void *xs0 = nullptr, *c1 = nullptr, *trunk = nullptr;
+    float *outb = nullptr, *flow[2] = {}, *rgb[2] = {}, *img = nullptr;
+
+    // scratch for the per-stage entry points (grow-only)
+    void *scr[3] = {};
+    size_t scr_sz[3] = {};
+
+    bool profile = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<float> times;
+
+    size_t act_size() const { return f16 ? 2 : 4; }
+    int out_res() const { return 8 << (ns - 1); }
+
+    bool hip_ok(hipError_t e, const char *what) {
+        if (e == hipSuccess) return true;
+        err = fmt("%s: %s", what, hipGetErrorString(e));
+        return false;
+    }
+    void *dalloc(size_t bytes, std::vector<void *> &list) {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes < 256 ? 256 : bytes) != hipSuccess) {
+            err = fmt("hipMalloc of %zu bytes failed", bytes);
+            return nullptr;
+        }
+        list.push_back(p);
+        return p;
+    }
+    template <typename T>
+    T *upload(const std::vector<T> &v) {
+        T *p = (T *) dalloc(v.size() * sizeof(T), allocs);
+        if (!p) return nullptr;
+        if (!hip_ok(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "upload"))
+            return nullptr;
+        return p;
+    }
+    // f32 values -> device act tensor (f16 RNE in f16 mode)
+    void *upload_act(const std::vector<float> &v) {
+        if (!f16) return upload(v);
+        std::vector<_Float16> h(v.size());
+        for (size_t i = 0; i < v.size(); i++) h[i] = (_Float16) v[i];
+        return upload(h);
+    }
+    const HostTensor *need(const std::string &name) {
+        auto it = host.find(name);
+        if (it == host.end()) {
+            if (err.empty()) err = "missing tensor " + name;
+            return nullptr;
+        }
+        return &it->second;
+    }
+    // device value of a tensor under the f16 keep rule (src/gguf_load.cpp:149-153)
+    std::vector<float> dev_value(const HostTensor &t) const {
+        std::vector<float> v = t.data;
+        if (f16 && (t.flags & TPMD_W_F16_FILE) && v.size() >= 4096)
+            for (auto &x : v) x = round_f16(x);
+        return v;
+    }
+    void *scratch(int i, size_t bytes) {
+        if (scr_sz[i] < bytes) {
+            if (scr[i]) (void) hipFree(scr[i]);
+            scr[i] = nullptr;
+            scr_sz[i] = 0;
+            if (hipMalloc(&scr[i], bytes) != hipSuccess) {
+                err = fmt("hipMalloc of %zu bytes failed", bytes);
+                return nullptr;
+            }
+            scr_sz[i] = bytes;
+        }
+        return scr[i];
+    }
+
+    std::string conv_name(int L) const {
+        return L == 0 ? std::string("dec.conv1") : fmt("dec.convs.%d", L - 1);
+    }
+
+    ~tpmd_ctx() {
+        if (device >= 0) (void) hipSetDevice(device);
+        for (auto e : ev) (void) hipEventDestroy(e);
+        for (void *p : allocs) (void) hipFree(p);
+        for (void *p : batch_allocs) (void) hipFree(p);
+        for (void *p : scr)
+            if (p) (void) hipFree(p);
+        if (stream) (void) hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+// motion_ae_scale restricted to dec.* tensors (src/motion_enc.cpp:14-45);
+// ne is the ggml order (reversed torch shape)
+double motion_ae_scale(const std::string &name, const std::vector<int64_t> &ne) {
+    const double SQRT2 = 1.4142135623730951;
+    auto ends_with = [&](const char *s) {
+        size_t n = strlen(s);
+        return name.size() >= n && name.compare(name.size() - n, n, s) == 0;
+    };
+    if (ends_with(".activate.bias") || (name.rfind("dec.to_rgbs.", 0) == 0 && ends_with(".conv.1.bias")))
+        return SQRT2;
+    if (!ends_with(".weight")) return 1.0;
+    if (name.rfind("dec.direction", 0) == 0 || ends_with("noise.weight")) return 1.0;
+    if (ends_with("modulation.weight")) return 1.0 / sqrt((double) ne[0]);
+    const double conv = 1.0 / sqrt((double) (ne[0] * ne[1] * ne[2]));
+    if (name.rfind("dec.to_rgbs.", 0) == 0 && ends_with(".conv.0.weight")) return conv * SQRT2;
+    if (ends_with(".conv.weight")) return conv;
+    return 1.0;
+}
+
+// expected torch shape of every decoder tensor for this config (Appendix of
+// the GGUF layout: src/motion_dec.cpp:17-29, tests/test_gguf.cpp:54-58)
+bool expected_shape(const tpmd_ctx *c, const std::string &name, std::vector<int64_t> &shape) {
+    const int C0 = c->ic[0];
+    auto is = [&](const std::string &s) { return name == s; };
+    if (is("dec.input.input")) { shape = {1, C0, 4, 4}; return true; }
+    if (is("dec.conv1.conv.weight")) { shape = {1, C0, C0, 3, 3}; return true; }
+    if (is("dec.conv1.conv.modulation.weight")) { shape = {C0, 512}; return true; }
+    if (is("dec.conv1.conv.modulation.bias") || is("dec.conv1.activate.bias")) { shape = {C0}; return true; }
+    for (int i = 0; i < 2 * c->ns; i++) {
+        const int j = i / 2;
+        const int cin = (i % 2 == 0) ? c->ic[j] : c->oc[j], cout = c->oc[j];
+        const std::string b = fmt("dec.convs.%d", i);
+        if (is(b + ".conv.weight")) { shape = {1, cout, cin, 3, 3}; return true; }
+        if (is(b + ".conv.modulation.weight")) { shape = {cin, 512}; return true; }
+        if (is(b + ".conv.modulation.bias")) { shape = {cin}; return true; }
+        if (is(b + ".activate.bias")) { shape = {cout}; return true; }
+        if (i % 2 == 0 && is(b + ".conv.blur.kernel")) { shape = {4, 4}; return true; }
+    }
+    for (int j = 0; j < c->ns; j++) {
+        const int C = c->oc[j];
+        const std::string f = fmt("dec.to_flows.%d", j), r = fmt("dec.to_rgbs.%d", j);
+        if (is(f + ".conv.weight")) { shape = {1, 3, C, 1, 1}; return true; }
+        if (is(f + ".conv.modulation.weight")) { shape = {C, 512}; return true; }
+        if (is(f + ".conv.modulation.bias")) { shape = {C}; return true; }
+        if (is(f + ".bias") || is(r + ".bias")) { shape = {1, 3, 1, 1}; return true; }
+        if (is(f + ".upsample.kernel") || is(r + ".upsample.kernel")) { shape = {4, 4}; return true; }
+        if (is(r + ".conv.0.weight")) { shape = {3, C, 1, 1}; return true; }
+        if (is(r + ".conv.1.bias")) { shape = {3}; return true; }
+    }
+    return false;
+}
+
+// dense cf GEMM matrix A[o][ic + IC*(kw + 3*kh)] (src/motion_dec.cpp:132-143)
+std::vector<float> make_acf(const std::vector<float> &W, int OC, int IC) {
+    const size_t R = (size_t) IC * 9;
+    std::vector<float> a((size_t) OC * R);
+    for (int o = 0; o < OC; o++)
+        for (int i = 0; i < IC; i++)
+            for (int kh = 0; kh < 3; kh++)
+                for (int kw = 0; kw < 3; kw++)
+                    a[(size_t) o * R + i + (size_t) IC * (kw + 3 * kh)] =
+                        W[((size_t) o * IC + i) * 9 + kh * 3 + kw];
+    return a;
+}
+
+// conv_transpose(3x3, s2) o Blur(4x4) as four 3x3 pad-1 kernels, one per
+// output parity class (by, bx); rows q = (2*by + bx)*OC + o, columns cf
+// ordered; double accumulation (src/motion_dec.cpp:144-186)
+std::vector<float> make_tsub(const std::vector<float> &W, const std::vector<float> &BK, int OC,
+                             int IC) {
+    const size_t R = (size_t) IC * 9;
+    std::vector<float> t((size_t) 4 * OC * R, 0.0f);
+    for (int o = 0; o < OC; o++)
+        for (int i = 0; i < IC; i++) {
+            const float *w = W.data() + ((size_t) o * IC + i) * 9;
+            for (int by = 0; by < 2; by++)
+                for (int bx = 0; bx < 2; bx++) {
+                    float *dst = t.data() + (size_t) ((2 * by + bx) * OC + o) * R;
+                    for (int ty = 0; ty < 3; ty++)
+                        for (int tx = 0; tx < 3; tx++) {
+                            const int dy = 1 - ty, dx = 1 - tx;
+                            double acc = 0;
+                            for (int cy = 0; cy < 3; cy++) {
+                                const int ay = 3 - by - 2 * dy - cy;
+                                if (ay < 0 || ay > 3) continue;
+                                for (int cx = 0; cx < 3; cx++) {
+                                    const int ax = 3 - bx - 2 * dx - cx;
+                                    if (ax < 0 || ax > 3) continue;
+                                    // flipped weight V[cy][cx] = W[2-cy][2-cx]
+                                    acc += (double) w[(2 - cy) * 3 + (2 - cx)] * (double) BK[ay * 4 + ax];
+                                }
+                            }
+                            dst[i + (size_t) IC * (tx + 3 * ty)] = (float) acc;
+                        }
+                }
+        }
+    return t;
+}
+
+// S_aug [OC][IC+1]: 0.5*sum_k W^2 (double), last column 0.5e-8
+// (src/motion_dec.cpp:113-122): folds the FusedLeakyReLU sqrt2 into 1/den
+std::vector<float> make_saug(const std::vector<float> &W, int OC, int IC) {
+    std::vector<float> s((size_t) OC * (IC + 1));
+    for (int o = 0; o < OC; o++) {
+        for (int i = 0; i < IC; i++) {
+            double a = 0;
+            const float *w = W.data() + ((size_t) o * IC + i) * 9;
+            for (int k = 0; k < 9; k++) a += (double) w[k] * w[k];
+            s[(size_t) o * (IC + 1) + i] = (float) (a * 0.5);
+        }
+        s[(size_t) o * (IC + 1) + IC] = 0.5e-8f;
+    }
+    return s;
+}
+
+bool check_ctx(tpmd_ctx *c) {
+    if (!c) return false;
+    c->err.clear();
+    if (hipSetDevice(c->device) != hipSuccess) {
+        c->err = "hipSetDevice failed";
+        return false;
+    }
+    return true;
+}
+
+hipStream_t pick_stream(tpmd_ctx *c, void *s) { return s ? (hipStream_t) s : c->stream; }
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+int tpmd_abi_version(void) { return TPMD_ABI_VERSION; }
+
+tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *stage_ic,
+                      const int *stage_oc) {
+    const std::string ft = ftype ? ftype : "f32";
+    if (ft != "f32" && ft != "f16") {
+        fprintf(stderr, "tpmd_create: ftype must be f32 or f16\n");
+        return nullptr;
+    }
+    if (n_stages < 1 || n_stages > TPMD_MAX_STAGES) {
+        fprintf(stderr, "tpmd_create: n_stages must be 1..7\n");
+        return nullptr;
+    }
+    if ((stage_ic == nullptr) != (stage_oc == nullptr)) {
+        fprintf(stderr, "tpmd_create: give both stage_ic and stage_oc or neither\n");
+        return nullptr;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        fprintf(stderr, "tpmd_create: no HIP device %d\n", device);
+        return nullptr;
+    }
+    tpmd_ctx *c = new (std::nothrow) tpmd_ctx();
+    if (!c) return nullptr;
+    c->device = device;
+    c->f16 = ft == "f16";
+    c->ns = n_stages;
+    for (int j = 0; j < 7; j++) {
+        c->ic[j] = stage_ic ? (j < n_stages ? stage_ic[j] : 0) : REF_IC[j];
+        c->oc[j] = stage_oc ? (j < n_stages ? stage_oc[j] : 0) : REF_OC[j];
+    }
+    const int kal = modconv_k_align(c->f16);
+    for (int j = 0; j < n_stages; j++) {
+        const int C = c->oc[j];
+        const bool c_ok = C == 32 || C == 64 || C == 128 || C == 256 || C == 512;
+        const bool ic_ok = c->ic[j] % kal == 0 && c->ic[j] % 32 == 0 && c->ic[j] >= 32;
+        const bool chain_ok = j == 0 || c->ic[j] == c->oc[j - 1];
+        if (!c_ok || !ic_ok || !chain_ok) {
+            fprintf(stderr,
+                    "tpmd_create: stage %d channels %d->%d unsupported (OC in {32..512} powers of "
+                    "two, IC multiple of 32, IC[j] == OC[j-1])\n",
+                    j, c->ic[j], c->oc[j]);
+            delete c;
+            return nullptr;
+        }
+    }
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        fprintf(stderr, "tpmd_create: stream creation failed\n");
+        delete c;
+        return nullptr;
+    }
+    return c;
+}
+
+void tpmd_destroy(tpmd_ctx *c) { delete c; }
+
+const char *tpmd_last_error(const tpmd_ctx *c) { return c ? c->err.c_str() : "no context"; }
+
+int tpmd_set_weight(tpmd_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+    if (!check_ctx(c)) return -1;
+    if (!name || !data || n <= 0) {
+        c->err = "tpmd_set_weight: null name/data or empty tensor";
+        return -1;
+    }
+    std::vector<int64_t> shape;
+    if (!expected_shape(c, name, shape)) {
+        c->err = fmt("tpmd_set_weight: unknown decoder tensor %s", name);
+        return -1;
+    }
+    int64_t want = 1;
+    for (auto d : shape) want *= d;
+    if (want != n) {
+        c->err = fmt("tpmd_set_weight: %s has %lld elements, expected %lld", name, (long long) n,
+                     (long long) want);
+        return -1;
+    }
+    std::vector<int64_t> ne(shape.rbegin(), shape.rend());
+    // the loader drops unit dims beyond 4 (src/gguf_load.cpp:111-124)
+    while (ne.size() > 4 && ne.back() == 1) ne.pop_back();
+    while (ne.size() < 4) ne.push_back(1);
+    HostTensor t;
+    t.data.assign(data, data + n);
+    t.flags = flags;
+    if (!(flags & TPMD_W_FOLDED)) {
+        const double s = motion_ae_scale(name, ne);
+        if (s != 1.0) {
+            const float fs = (float) s;
+            for (auto &v : t.data) v *= fs;
+        }
+    }
+    c->host[name] = std::move(t);
+    c->prepared = false;
+    return 0;
+}
+
+int tpmd_prepare(tpmd_ctx *c) {
+    if (!check_ctx(c)) return -1;
+    for (void *p : c->allocs) (void) hipFree(p);
+    c->allocs.clear();
+    c->prepared = false;
+    const int ns = c->ns, C0 = c->ic[0];
+
+    // ---- convs: conv1 + 2 per stage
+    c->nconv = 1 + 2 * ns;
+    std::vector<float> saug_all, wmod, bmod;
+    int seg = 0;
+    c->R_total = 0;
+    auto add_style = [&](const std::string &base, int width) -> int {
+        const HostTensor *mw = c->need(base + ".modulation.weight");
+        const HostTensor *mb = c->need(base + ".modulation.bias");
+        if (!mw || !mb) return -1;
+        std::vector<float> v = c->dev_value(*mw);
+        wmod.insert(wmod.end(), v.begin(), v.end());
+        bmod.insert(bmod.end(), mb->data.begin(), mb->data.end());
+        c->seg_width[seg] = width;
+        c->R_total += width;
+        return seg++;
+    };
+    for (int L = 0; L < c->nconv; L++) {
+        ConvW &cv = c->conv[L];
+        const std::string base = c->conv_name(L);
+        const int j = (L - 1) / 2;
+        cv.up = L > 0 && (L - 1) % 2 == 0;
+        cv.ic = L == 0 ? C0 : (cv.up ? c->ic[j] : c->oc[j]);
+        cv.oc = L == 0 ? C0 : c->oc[j];
+        const HostTensor *W = c->need(base + ".conv.weight");
+        const HostTensor *ab = c->need(base + ".activate.bias");
+        if (!W || !ab) return -1;
+        cv.seg = add_style(base + ".conv", cv.ic);
+        if (cv.seg < 0) return -1;
+        std::vector<float> sa = make_saug(W->data, cv.oc, cv.ic);
+        cv.saug_off = (int64_t) saug_all.size();
+        saug_all.insert(saug_all.end(), sa.begin(), sa.end());
+        if (cv.up) {
+            const HostTensor *bk = c->need(base + ".conv.blur.kernel");
+            if (!bk) return -1;
+            cv.A = c->upload_act(make_tsub(W->data, bk->data, cv.oc, cv.ic));
+        } else {
+            // conv1 uses its weight tensor as stored (f16-kept values); the
+            // dense convs use the derived acf (f16 whenever ftype is f16)
+            std::vector<float> wv = L == 0 ? c->dev_value(*W) : W->data;
+            cv.A = c->upload_act(make_acf(wv, cv.oc, cv.ic));
+        }
+        cv.bias = c->upload(ab->data);
+        if (!cv.A || !cv.bias) return -1;
+    }
+    for (int j = 0; j < ns; j++) {
+        StageW &s = c->st[j];
+        const int C = c->oc[j], r = 8 << j;
+        const std::string f = fmt("dec.to_flows.%d", j), rb = fmt("dec.to_rgbs.%d", j);
+        const HostTensor *fw = c->need(f + ".conv.weight"), *fb = c->need(f + ".bias"),
+                         *fu = c->need(f + ".upsample.kernel"), *rw = c->need(rb + ".conv.0.weight"),
+                         *rl = c->need(rb + ".conv.1.bias"), *rbs = c->need(rb + ".bias"),
+                         *ru = c->need(rb + ".upsample.kernel");
+        if (!fw || !fb || !fu || !rw || !rl || !rbs || !ru) return -1;
+        s.seg = add_style(f + ".conv", C);
+        if (s.seg < 0) return -1;
+        s.wflow = c->upload(c->dev_value(*fw));
+        s.fbias = c->upload(fb->data);
+        s.fup = c->upload(fu->data);
+        s.wrgb = c->upload(c->dev_value(*rw));
+        s.rlb = c->upload(rl->data);
+        s.rbias = c->upload(rbs->data);
+        s.rup = c->upload(ru->data);
+        std::vector<float> lin((size_t) r);
+        for (int i = 0; i < r; i++) lin[(size_t) i] = (float) (-1.0 + 2.0 * i / (r - 1));
+        s.lin = c->upload(lin);
+        if (!s.wflow || !s.fbias || !s.fup || !s.wrgb || !s.rlb || !s.rbias || !s.rup || !s.lin)
+            return -1;
+        (void) C;
+    }
+    c->nseg = seg;
+    {
+        const HostTensor *in = c->need("dec.input.input");
+        if (!in) return -1;
+        std::vector<float> v = c->dev_value(*in), cl((size_t) 16 * C0);
+        for (int ch = 0; ch < C0; ch++)
+            for (int p = 0; p < 16; p++) cl[(size_t) p * C0 + ch] = v[(size_t) ch * 16 + p];
+        c->input_cl = c->upload(cl);
+    }
+    c->wmod = c->upload(wmod);
+    c->bmod = c->upload(bmod);
+    c->saug_all = c->upload(saug_all);
+    if (!c->input_cl || !c->wmod || !c->bmod || !c->saug_all) return -1;
+    c->prepared = true;
+    c->built = false;
+    c->feats_set = false;
+    return 0;
+}
+
+int tpmd_build(tpmd_ctx *c, int max_batch) {
+    if (!check_ctx(c)) return -1;
+    if (!c->prepared) {
+        c->err = "decoder not prepared";
+        return -1;
+    }
+    if (max_batch < 1 || max_batch > 256) {
+        c->err = "max_batch must be 1..256";
+        return -1;
+    }
+    for (void *p : c->batch_allocs) (void) hipFree(p);
+    c->batch_allocs.clear();
+    c->built = false;
+    c->feats_set = false;
+    const int B = max_batch, ns = c->ns, C0 = c->ic[0];
+    c->batch = B;
+
+    // style segment table: block [B][width] per segment
+    SegTable &sg = c->seg;
+    sg.n = c->nseg;
+    int64_t off = 0;
+    int row = 0;
+    for (int i = 0; i < c->nseg; i++) {
+        sg.row0[i] = row;
+        sg.width[i] = c->seg_width[i];
+        sg.out0[i] = off;
+        row += c->seg_width[i];
+        off += (int64_t) B * c->seg_width[i];
+    }
+    sg.row0[c->nseg] = row;
+    const int64_t s_total = off;
+    DemodTable &dt = c->dem;
+    dt.n = c->nconv;
+    int64_t doff = 0;
+    row = 0;
+    for (int L = 0; L < c->nconv; L++) {
+        ConvW &cv = c->conv[L];
+        cv.s_off = sg.out0[cv.seg];
+        cv.d_off = doff;
+        dt.row0[L] = row;
+        dt.ic[L] = cv.ic;
+        dt.oc[L] = cv.oc;
+        dt.saug0[L] = cv.saug_off;
+        dt.s0[L] = cv.s_off;
+        dt.d0[L] = doff;
+        row += cv.oc;
+        doff += (int64_t) B * cv.oc;
+    }
+    dt.row0[c->nconv] = row;
+    for (int j = 0; j < ns; j++) c->st[j].s_off = sg.out0[c->st[j].seg];
+
+    size_t act_max = (size_t) 16 * C0, out_max = 0, skip_max = 1;
+    for (int j = 0; j < ns; j++) {
+        const size_t r = (size_t) 8 << j;
+        act_max = std::max(act_max, r * r * c->oc[j]);
+        out_max = std::max(out_max, r * r * c->oc[j]);
+        if (j + 1 < ns) skip_max = std::max(skip_max, 3 * r * r);
+    }
+    const size_t R = (size_t) c->out_res();
+    auto A = [&](size_t bytes) { return c->dalloc(bytes, c->batch_allocs); };
+    c->lat = (float *) A((size_t) B * 512 * 4);
+    c->s_all = (float *) A((size_t) s_total * 4);
+    c->den_all = (float *) A((size_t) doff * 4);
+    c->xs0 = A((size_t) B * 16 * C0 * c->act_size());
+    c->c1 = A((size_t) B * act_max * c->act_size());
+    c->trunk = A((size_t) B * act_max * c->act_size());
+    c->outb = (float *) A((size_t) B * out_max * 4);
+    for (int i = 0; i < 2; i++) {
+        c->flow[i] = (float *) A((size_t) B * skip_max * 4);
+        c->rgb[i] = (float *) A((size_t) B * skip_max * 4);
+    }
+    c->img = (float *) A((size_t) B * 3 * R * R * 4);
+    if (!c->lat || !c->s_all || !c->den_all || !c->xs0 || !c->c1 || !c->trunk || !c->outb ||
+        !c->flow[0] || !c->flow[1] || !c->rgb[0] || !c->rgb[1] || !c->img)
+        return -1;
+    for (int j = 0; j < ns; j++) {
+        const size_t r = (size_t) 8 << j;
+        c->st[j].feat = A(r * r * c->oc[j] * c->act_size());
+        if (!c->st[j].feat) return -1;
+        if (!c->hip_ok(hipMemset(c->st[j].feat, 0, r * r * c->oc[j] * c->act_size()), "memset"))
+            return -1;
+    }
+    c->built = true;
+    return 0;
+}
+
+int tpmd_batch(const tpmd_ctx *c) { return c ? c->batch : 0; }
+int tpmd_out_res(const tpmd_ctx *c) { return c ? c->out_res() : 0; }
+
+static int set_feats_impl(tpmd_ctx *c, const float *const *feats, bool dev) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built) {
+        c->err = "decoder not built";
+        return -1;
+    }
+    if (!feats) {
+        c->err = "feat size mismatch";
+        return -1;
+    }
+    for (int j = 0; j < c->ns; j++) {
+        if (!feats[j]) {
+            c->err = "feat size mismatch";
+            return -1;
+        }
+        const size_t r = (size_t) 8 << j, n = r * r * c->oc[j];
+        float *tmp = (float *) c->scratch(0, n * 4);
+        if (!tmp) return -1;
+        if (!c->hip_ok(hipMemcpyAsync(tmp, feats[j], n * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                      c->stream), "feat upload"))
+            return -1;
+        if (!c->hip_ok(launch_prescale_map(c->f16, tmp, nullptr, c->st[j].feat, c->oc[j], (int64_t) r * r, 1,
+                                           c->stream), "feat convert"))
+            return -1;
+        if (!c->hip_ok(hipStreamSynchronize(c->stream), "feat sync")) return -1;
+    }
+    c->feats_set = true;
+    return 0;
+}
+
+int tpmd_set_feats(tpmd_ctx *c, const float *const *feats) { return set_feats_impl(c, feats, false); }
+int tpmd_set_feats_device(tpmd_ctx *c, const float *const *feats) { return set_feats_impl(c, feats, true); }
+
+static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
+    hipStream_t st = c->stream;
+    const bool f16 = c->f16;
+    const int ns = c->ns, C0 = c->ic[0];
+    int slot = 0;
+    auto mark = [&]() {
+        if (c->profile) (void) hipEventRecord(c->ev[(size_t) slot++], st);
+    };
+    mark();
+    if (!c->hip_ok(launch_style_gemv(c->wmod, c->bmod, c->lat, c->s_all, c->seg, n, st), "style")) return false;
+    if (!c->hip_ok(launch_demod(c->saug_all, c->s_all, c->den_all, c->dem, n, st), "demod")) return false;
+    const ConvW &k1 = c->conv[0];
+    if (!c->hip_ok(launch_prescale_input(f16, c->input_cl, c->s_all + k1.s_off, c->xs0, C0, n, st), "prescale"))
+        return false;
+    // conv1 -> trunk (pre-scaled by the stage-0 up-conv style)
+    if (!c->hip_ok(launch_modconv(0, f16, f16, k1.A, c->xs0, c->trunk, c->den_all + k1.d_off, k1.bias,
+                                  c->s_all + c->conv[1].s_off, n, 4, 4, C0, C0, (int64_t) 16 * C0, st),
+                   "conv1"))
+        return false;
+    for (int j = 0; j < ns; j++) {
+        const int r = 8 << j, rh = r / 2, C = c->oc[j], IC = c->ic[j];
+        const bool last = j + 1 == ns;
+        const ConvW &up = c->conv[1 + 2 * j], &dn = c->conv[2 + 2 * j];
+        mark();
+        if (!c->hip_ok(launch_modconv(1, f16, f16, up.A, c->trunk, c->c1, c->den_all + up.d_off, up.bias,
+                                      c->s_all + dn.s_off, n, rh, rh, IC, C, (int64_t) rh * rh * IC, st),
+                       "up-conv"))
+            return false;
+        mark();
+        if (!c->hip_ok(launch_modconv(0, f16, false, dn.A, c->c1, c->outb, c->den_all + dn.d_off, dn.bias,
+                                      nullptr, n, r, r, C, C, (int64_t) r * r * C, st),
+                       "conv"))
+            return false;
+        mark();
+        const StageW &s = c->st[j];
+        TailArgs a{};
+        a.out = c->outb;
+        a.feat = s.feat;
+        a.wflow = s.wflow;
+        a.sflow = c->s_all + s.s_off;
+        a.fbias = s.fbias;
+        a.fup = s.fup;
+        a.flow_prev = j > 0 ? c->flow[(j - 1) & 1] : nullptr;
+        a.flow_cur = last ? nullptr : c->flow[j & 1];
+        a.lin = s.lin;
+        a.wrgb = s.wrgb;
+        a.rlb = s.rlb;
+        a.rbias = s.rbias;
+        a.rup = s.rup;
+        a.rgb_prev = j > 0 ? c->rgb[(j - 1) & 1] : nullptr;
+        a.rgb_cur = last ? img_dst : c->rgb[j & 1];
+        a.s_next = last ? nullptr : c->s_all + c->conv[3 + 2 * j].s_off;
+        a.trunk = last ? nullptr : c->trunk;
+        a.warp_tap = nullptr;
+        a.nframes = n;
+        a.r = r;
+        a.C = C;
+        if (!c->hip_ok(launch_stage_tail(a, f16, false, f16, st), "tail")) return false;
+    }
+    mark();
+    return true;
+}
+
+int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built) {
+        c->err = "decoder not built";
+        return -1;
+    }
+    if (!c->feats_set) {
+        c->err = "feats not set";
+        return -1;
+    }
+    if (!styles || n < 1 || n > c->batch) {
+        c->err = fmt("decode_batch: need 1..%d styles", c->batch);
+        return -1;
+    }
+    const size_t R = (size_t) c->out_res();
+    const hipMemcpyKind k_in = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    if (!c->hip_ok(hipMemcpyAsync(c->lat, styles, (size_t) n * 512 * 4, k_in, c->stream), "style upload"))
+        return -1;
+    if (c->profile) {
+        const size_t need = (size_t) 2 + 3 * c->ns;
+        while (c->ev.size() < need) {
+            hipEvent_t e;
+            if (!c->hip_ok(hipEventCreate(&e), "event")) return -1;
+            c->ev.push_back(e);
+        }
+    }
+    float *dst = (on_device && imgs) ? imgs : c->img;
+    if (!enqueue_decode(c, n, dst)) return -1;
+    if (!on_device) {
+        if (imgs && !c->hip_ok(hipMemcpyAsync(imgs, c->img, (size_t) n * 3 * R * R * 4, hipMemcpyDeviceToHost,
+                                              c->stream), "image download"))
+            return -1;
+        if (!c->hip_ok(hipStreamSynchronize(c->stream), "decode")) return -1;
+    }
+    if (c->profile) {
+        if (!c->hip_ok(hipStreamSynchronize(c->stream), "decode")) return -1;
+        const size_t ns = (size_t) 1 + 3 * c->ns;
+        c->times.assign(ns, 0.0f);
+        for (size_t i = 0; i < ns; i++) {
+            float ms = 0;
+            (void) hipEventElapsedTime(&ms, c->ev[i], c->ev[i + 1]);
+            c->times[i] = ms * 1000.0f;
+        }
+    }
+    return 0;
+}
+
+int tpmd_decode(tpmd_ctx *c, const float *style, float *img) {
+    return tpmd_decode_batch(c, style, 1, img, 0);
+}
+
+int tpmd_sync(tpmd_ctx *c) {
+    if (!check_ctx(c)) return -1;
+    return c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
+}
+
+int tpmd_profile_stages(tpmd_ctx *c, int enable) {
+    if (!check_ctx(c)) return -1;
+    c->profile = enable != 0;
+    return 1 + 3 * c->ns;
+}
+
+int tpmd_stage_times(const tpmd_ctx *c, float *us, int max_slots) {
+    if (!c || !us) return -1;
+    const int n = (int) c->times.size() < max_slots ? (int) c->times.size() : max_slots;
+    for (int i = 0; i < n; i++) us[i] = c->times[(size_t) i];
+    return n;
+}
+
+int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
+                 void *stream) {
+    if (!check_ctx(c)) return -1;
+    if (!c->prepared) {
+        c->err = "decoder not prepared";
+        return -1;
+    }
+    if (conv < 0 || conv >= c->nconv || !x || !s || !y || n < 1 || H < 1 || W < 1) {
+        c->err = "tpmd_modconv: bad arguments";
+        return -1;
+    }
+    const ConvW &cv = c->conv[conv];
+    hipStream_t st = pick_stream(c, stream);
+    const int64_t npix = (int64_t) H * W;
+    void *xs = c->scratch(1, (size_t) n * npix * cv.ic * c->act_size());
+    float *den = (float *) c->scratch(2, (size_t) n * cv.oc * 4);
+    if (!xs || !den) return -1;
+    DemodTable t{};
+    t.n = 1;
+    t.row0[0] = 0;
+    t.row0[1] = cv.oc;
+    t.ic[0] = cv.ic;
+    t.oc[0] = cv.oc;
+    t.saug0[0] = cv.saug_off;
+    t.s0[0] = 0;
+    t.d0[0] = 0;
+    if (!c->hip_ok(launch_demod(c->saug_all, s, den, t, n, st), "demod")) return -1;
+    if (!c->hip_ok(launch_prescale_map(c->f16, x, s, xs, cv.ic, npix, n, st), "prescale")) return -1;
+    if (!c->hip_ok(launch_modconv(cv.up ? 1 : 0, c->f16, false, cv.A, xs, y, den, cv.bias, nullptr, n, H, W,
+                                  cv.ic, cv.oc, npix * cv.ic, st),
+                   "modconv"))
+        return -1;
+    return 0;
+}
+
+int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
+                    const float *rgb_prev, float *flow, float *trunk, float *rgb, float *warp,
+                    void *stream) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built || !c->feats_set) {
+        c->err = "decoder not built / feats not set";
+        return -1;
+    }
+    if (j < 0 || j >= c->ns || !out || !s_flow || !rgb || n < 1) {
+        c->err = "tpmd_stage_tail: bad arguments";
+        return -1;
+    }
+    if (j > 0 && (!flow_prev || !rgb_prev)) {
+        c->err = "tpmd_stage_tail: stages > 0 need flow_prev and rgb_prev";
+        return -1;
+    }
+    const StageW &s = c->st[j];
+    TailArgs a{};
+    a.out = out;
+    a.feat = s.feat;
+    a.wflow = s.wflow;
+    a.sflow = s_flow;
+    a.fbias = s.fbias;
+    a.fup = s.fup;
+    a.flow_prev = j > 0 ? flow_prev : nullptr;
+    a.flow_cur = flow;
+    a.lin = s.lin;
+    a.wrgb = s.wrgb;
+    a.rlb = s.rlb;
+    a.rbias = s.rbias;
+    a.rup = s.rup;
+    a.rgb_prev = j > 0 ? rgb_prev : nullptr;
+    a.rgb_cur = rgb;
+    a.s_next = nullptr;
+    a.trunk = trunk;
+    a.warp_tap = warp;
+    a.nframes = n;
+    a.r = 8 << j;
+    a.C = c->oc[j];
+    return c->hip_ok(launch_stage_tail(a, c->f16, false, false, pick_stream(c, stream)), "tail") ? 0 : -1;
+}
+
+// ---- op-level
+
+int tpmd_gather(const void *feat, int feat_f16, int C, int W, int H, const float *grid, int64_t N,
+                int planar, int sp, float *dst, void *stream) {
+    if (!feat || !grid || !dst || C < 1 || W < 1 || H < 1 || N < 0) return -1;
+    return launch_gather(feat, feat_f16 != 0, grid, dst, C, W, H, N, planar, sp, (hipStream_t) stream) ==
+                   hipSuccess
+               ? 0
+               : -1;
+}
+
+int tpmd_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0, int32_t *y0,
+                     float *wx, float *wy, void *stream) {
+    if (!grid || !x0 || !y0 || !wx || !wy || W < 1 || H < 1 || N < 0) return -1;
+    return launch_gather_taps(grid, W, H, N, planar, x0, y0, wx, wy, (hipStream_t) stream) == hipSuccess ? 0
+                                                                                                      : -1;
+}
+
+int tpmd_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB, void *stream) {
+    if (!x || !k4 || !y || W < 1 || H < 1 || CB < 0) return -1;
+    return launch_upfirdn2x(x, k4, y, W, H, CB, (hipStream_t) stream) == hipSuccess ? 0 : -1;
+}
+
+int tpmd_flow_grid(const float *fl, const float *xs, float *y, int64_t N, void *stream) {
+    if (!fl || !xs || !y || N < 0) return -1;
+    return launch_flow_grid(fl, xs, y, N, (hipStream_t) stream) == hipSuccess ? 0 : -1;
+}
+
+}  // extern "C"

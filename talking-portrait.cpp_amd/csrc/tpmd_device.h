@@ -1,0 +1,103 @@
+// Device-side building blocks shared by the motion-decoder kernels (gfx950).
+//
+// Conventions:
+//   * activations are channel-last ("CL"): [frame][y][x][channel], the
+//     channel dimension contiguous, matching the reference's [C, N, B]
+//     fast-graph layout (src/motion_dec.cpp:240-241);
+//   * skip pyramids (rgb, flow) are per-frame planes [frame][3][y][x] f32,
+//     the reference's spatial [W, H, 3, B] layout;
+//   * "act_t" is the storage type of conv operands: _Float16 in f16 mode
+//     (f16 in, f32 accumulate), float in f32 mode.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tpmd {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr float kSlope = 0.2f;
+
+__device__ __forceinline__ float leaky(float v) { return v > 0.0f ? v : kSlope * v; }
+
+// 16-byte vector of act_t and its element count
+template <typename T> struct vec16;
+template <> struct vec16<float> {
+    typedef floatx4 type;
+    static constexpr int n = 4;
+};
+template <> struct vec16<half_t> {
+    typedef half8 type;
+    static constexpr int n = 8;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(half_t v) { return (float) v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ half_t from_f32<half_t>(float v) { return (half_t) v; }
+
+// sum over aligned groups of G lanes (G a power of two <= 64), result in
+// every lane of the group: butterfly over DPP-able xor shuffles
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// upfirdn2d(up=2, pad=(2,1)) of one SP plane at output (X, Y), 4x4 kernel
+// k4[i + 4j] (patch :996-1018 semantics): the zero-stuffed window hits at
+// most 2x2 source pixels; accumulation order j-major, i-minor, skipping the
+// zero-stuffed taps exactly like the reference loop.
+__device__ __forceinline__ float upfirdn2x_at(const float *__restrict__ plane, int W, int H,
+                                              const float *__restrict__ k4, int X, int Y) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int vy = Y + j - 2;
+        if (vy < 0 || vy >= 2 * H || (vy & 1)) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int vx = X + i - 2;
+            if (vx < 0 || vx >= 2 * W || (vx & 1)) continue;
+            acc += plane[(vx >> 1) + W * (vy >> 1)] * k4[i + 4 * j];
+        }
+    }
+    return acc;
+}
+
+// grid_sample (bilinear, zeros, align_corners=False) tap geometry for one
+// point, computed with one rounding per operation (patch :688-718):
+//   fx = (gx + 1) * 0.5 * W - 0.5,  x0 = floor(fx),  wx = fx - x0
+struct taps4 {
+    int x0, y0;
+    float wx, wy;
+};
+__device__ __forceinline__ taps4 gather_geometry(float gx, float gy, int W, int H) {
+#pragma clang fp contract(off)
+    taps4 t;
+    const float fx = (gx + 1.0f) * 0.5f * (float) W - 0.5f;
+    const float fy = (gy + 1.0f) * 0.5f * (float) H - 0.5f;
+    const float fxf = floorf(fx), fyf = floorf(fy);
+    t.x0 = (int) fxf;
+    t.y0 = (int) fyf;
+    t.wx = fx - fxf;
+    t.wy = fy - fyf;
+    return t;
+}
+
+// weight of tap k (cx = x0 + (k&1), cy = y0 + (k>>1))
+__device__ __forceinline__ float tap_weight(const taps4 &t, int k) {
+#pragma clang fp contract(off)
+    return ((k & 1) ? t.wx : 1.0f - t.wx) * ((k >> 1) ? t.wy : 1.0f - t.wy);
+}
+
+}  // namespace tpmd

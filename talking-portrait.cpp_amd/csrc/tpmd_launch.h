@@ -1,0 +1,78 @@
+// Host-callable kernel launchers of the motion-decoder library (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tpmd {
+
+constexpr int kMaxSeg = 32;
+
+// style GEMV: global row -> (conv segment, row within it, output offset)
+struct SegTable {
+    int n;                    // segments
+    int row0[kMaxSeg + 1];    // first global row of each segment; row0[n] = total
+    int width[kMaxSeg];       // rows of the segment (= channels of the style)
+    int64_t out0[kMaxSeg];    // element offset of the segment's [frame][width] block
+};
+
+// demodulation: global row -> (demod conv, output channel)
+struct DemodTable {
+    int n;
+    int row0[kMaxSeg + 1];
+    int ic[kMaxSeg], oc[kMaxSeg];
+    int64_t saug0[kMaxSeg];   // element offset of the conv's S_aug [OC][IC+1]
+    int64_t s0[kMaxSeg];      // element offset of its style block [frame][IC]
+    int64_t d0[kMaxSeg];      // element offset of its 1/den block [frame][OC]
+};
+
+struct TailArgs {
+    const void *out;          // CL [frame][r*r][C] dense-conv output (TOUT)
+    const void *feat;         // [r*r][C] warp features (TF)
+    const float *wflow;       // [3][C] ToFlow weight (scale-folded)
+    const float *sflow;       // [frame][C] ToFlow style
+    const float *fbias;       // [3]
+    const float *fup;         // [16] upsample kernel (x4 gain)
+    const float *flow_prev;   // SP [frame][3][r/2][r/2] or null
+    float *flow_cur;          // SP [frame][3][r][r] or null
+    const float *lin;         // [r] identity grid coordinates
+    const float *wrgb;        // [3][C] ToRGB weight (scale-folded)
+    const float *rlb;         // [3] ToRGB FusedLeakyReLU bias (x sqrt2)
+    const float *rbias;       // [3] ToRGB output bias
+    const float *rup;         // [16]
+    const float *rgb_prev;    // SP [frame][3][r/2][r/2] or null
+    float *rgb_cur;           // SP [frame][3][r][r]
+    const float *s_next;      // [frame][C] style of the next up-conv, or null
+    void *trunk;              // CL [frame][r*r][C] (TT) or null
+    float *warp_tap;          // CL [frame][r*r][C] f32 or null (tests)
+    int nframes, r, C;
+};
+
+hipError_t launch_gather(const void *feat, bool feat_f16, const float *grid, float *dst, int C,
+                         int W, int H, int64_t N, int planar, int sp, hipStream_t st);
+hipError_t launch_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0,
+                              int32_t *y0, float *wx, float *wy, hipStream_t st);
+hipError_t launch_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB,
+                            hipStream_t st);
+hipError_t launch_flow_grid(const float *fl, const float *xs, float *y, int64_t N,
+                            hipStream_t st);
+
+int modconv_k_align(bool f16);
+hipError_t launch_modconv(int mode, bool f16, bool out_f16, const void *A, const void *X, void *Y,
+                          const float *inv_den, const float *bias, const float *out_scale,
+                          int nframes, int H, int W, int IC, int OC, int64_t x_bstride,
+                          hipStream_t st);
+
+hipError_t launch_stage_tail(const TailArgs &a, bool feat_f16, bool out_f16, bool trunk_f16,
+                             hipStream_t st);
+
+hipError_t launch_style_gemv(const float *Wm, const float *bm, const float *lat, float *s,
+                             const SegTable &seg, int nframes, hipStream_t st);
+hipError_t launch_demod(const float *saug, const float *s, float *inv_den, const DemodTable &t,
+                        int nframes, hipStream_t st);
+hipError_t launch_prescale_input(bool f16, const float *in, const float *s, void *xs, int C,
+                                 int nframes, hipStream_t st);
+hipError_t launch_prescale_map(bool f16, const float *x, const float *s, void *xs, int C,
+                               int64_t npix_per_frame, int nframes, hipStream_t st);
+
+}  // namespace tpmd

@@ -1,0 +1,268 @@
+"""Python binding of libtpmd.so (ctypes), the MI355X motion decoder.
+
+A thin host mirror of the reference's tp::motion_dec interface
+(src/motion_dec.h:34-47) over the C ABI of include/tpmd.h:
+
+    dec = MotionDecoder(ftype="f16")          # tpmd_create
+    dec.set_weights(raw)                       # weights_t::load, dec.* tensors
+    dec.prepare()                              # motion_dec::prepare
+    dec.build(batch=16)                        # motion_dec::build
+    dec.set_feats(feats)                       # motion_dec::set_feats
+    imgs = dec.decode_batch(styles)            # motion_dec::decode_batch
+
+Errors raise TpmdError carrying tpmd_last_error(), the reference's
+`false + err` contract.  Device buffers are torch tensors (PyTorch is used
+only for device memory and streams).  The library is required: importing
+this module without libtpmd.so built raises, there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtpmd.so")
+HEADER = os.path.join(os.path.dirname(_HERE), "include", "tpmd.h")
+
+W_F16_FILE = 1
+W_FOLDED = 2
+
+
+class TpmdError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TpmdError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, I64, C = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_char_p
+        sig = {
+            "tpmd_abi_version": (I, []),
+            "tpmd_create": (P, [I, C, I, P, P]),
+            "tpmd_destroy": (None, [P]),
+            "tpmd_last_error": (C, [P]),
+            "tpmd_set_weight": (I, [P, C, P, I64, I]),
+            "tpmd_prepare": (I, [P]),
+            "tpmd_build": (I, [P, I]),
+            "tpmd_batch": (I, [P]),
+            "tpmd_out_res": (I, [P]),
+            "tpmd_set_feats": (I, [P, P]),
+            "tpmd_set_feats_device": (I, [P, P]),
+            "tpmd_decode_batch": (I, [P, P, I, P, I]),
+            "tpmd_decode": (I, [P, P, P]),
+            "tpmd_sync": (I, [P]),
+            "tpmd_profile_stages": (I, [P, I]),
+            "tpmd_stage_times": (I, [P, P, I]),
+            "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
+            "tpmd_stage_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P]),
+            "tpmd_gather": (I, [P, I, I, I, I, P, I64, I, I, P, P]),
+            "tpmd_gather_taps": (I, [P, I, I, I64, I, P, P, P, P, P]),
+            "tpmd_upfirdn2x": (I, [P, P, P, I, I, I64, P]),
+            "tpmd_flow_grid": (I, [P, P, P, I64, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def header_symbols():
+    """Function names declared in include/tpmd.h."""
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(tpmd_[a-z0-9_]+)\s*\(", txt)))
+
+
+def _ptr(t):
+    """device pointer of a torch tensor (or None)"""
+    if t is None:
+        return None
+    assert t.is_contiguous(), "tensors passed to the library must be contiguous"
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _hptr(a):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _stream(stream):
+    if stream is None:
+        return None
+    return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+class MotionDecoder:
+    """The decoder context (tpmd_ctx)."""
+
+    def __init__(self, ftype="f32", n_stages=7, ic=None, oc=None, device=0):
+        L = lib()
+        self.ftype = ftype
+        self.n_stages = n_stages
+        if ic is not None:
+            self._ic = (ctypes.c_int * n_stages)(*ic)
+            self._oc = (ctypes.c_int * n_stages)(*oc)
+            self.ic, self.oc = tuple(ic), tuple(oc)
+        else:
+            self._ic = self._oc = None
+            self.ic = (512, 512, 512, 512, 256, 128, 64)[:n_stages]
+            self.oc = (512, 512, 512, 256, 128, 64, 32)[:n_stages]
+        h = L.tpmd_create(device, ftype.encode(), n_stages,
+                          ctypes.cast(self._ic, ctypes.c_void_p) if self._ic else None,
+                          ctypes.cast(self._oc, ctypes.c_void_p) if self._oc else None)
+        if not h:
+            raise TpmdError("tpmd_create failed (see stderr)")
+        self.h = ctypes.c_void_p(h)
+        self.batch = 0
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().tpmd_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != 0:
+            raise TpmdError(lib().tpmd_last_error(self.h).decode())
+        return rc
+
+    @property
+    def last_error(self):
+        return lib().tpmd_last_error(self.h).decode()
+
+    # ---- lifecycle
+    def set_weight(self, name, arr, f16_file=False, folded=False):
+        a = np.ascontiguousarray(arr, dtype=np.float32)
+        flags = (W_F16_FILE if f16_file else 0) | (W_FOLDED if folded else 0)
+        self._check(lib().tpmd_set_weight(self.h, name.encode(), _hptr(a), a.size, flags))
+
+    def set_weights(self, raw):
+        for name, (arr, f16) in raw.items():
+            self.set_weight(name, arr, f16_file=f16)
+
+    def prepare(self):
+        self._check(lib().tpmd_prepare(self.h))
+
+    def build(self, batch):
+        self._check(lib().tpmd_build(self.h, int(batch)))
+        self.batch = lib().tpmd_batch(self.h)
+        self.res = lib().tpmd_out_res(self.h)
+
+    def set_feats(self, feats):
+        arrs = [np.ascontiguousarray(f, dtype=np.float32) for f in feats]
+        ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+        self._check(lib().tpmd_set_feats(self.h, ctypes.cast(ptrs, ctypes.c_void_p)))
+
+    def set_feats_device(self, feats):
+        ptrs = (ctypes.c_void_p * len(feats))(*[f.data_ptr() for f in feats])
+        self._check(lib().tpmd_set_feats_device(self.h, ctypes.cast(ptrs, ctypes.c_void_p)))
+
+    # ---- decode
+    def decode_batch(self, styles):
+        """host (n, 512) float32 -> host (n, 3, R, R) float32 (synchronous)"""
+        s = np.ascontiguousarray(styles, dtype=np.float32).reshape(-1, 512)
+        n = s.shape[0]
+        out = np.empty((n, 3, self.res, self.res), np.float32)
+        self._check(lib().tpmd_decode_batch(self.h, _hptr(s), n, _hptr(out), 0))
+        return out
+
+    def decode_batch_device(self, styles_dev, imgs_dev):
+        """device (n, 512) -> device (n, 3, R, R), enqueued on the decoder stream"""
+        n = styles_dev.shape[0]
+        self._check(lib().tpmd_decode_batch(self.h, _ptr(styles_dev), n, _ptr(imgs_dev), 1))
+
+    def decode(self, style):
+        s = np.ascontiguousarray(style, dtype=np.float32).reshape(512)
+        out = np.empty((3, self.res, self.res), np.float32)
+        self._check(lib().tpmd_decode(self.h, _hptr(s), _hptr(out)))
+        return out
+
+    def sync(self):
+        self._check(lib().tpmd_sync(self.h))
+
+    def profile_stages(self, enable=True):
+        return lib().tpmd_profile_stages(self.h, 1 if enable else 0)
+
+    def stage_times(self):
+        buf = (ctypes.c_float * 64)()
+        n = lib().tpmd_stage_times(self.h, buf, 64)
+        return list(buf[:max(n, 0)])
+
+    # ---- per-stage entry points (torch cuda tensors)
+    def modconv(self, conv, x, s, y, stream=None):
+        n, H, W, _ = x.shape
+        self._check(lib().tpmd_modconv(self.h, conv, _ptr(x), n, H, W, _ptr(s), _ptr(y), _stream(stream)))
+
+    def stage_tail(self, j, out, s_flow, flow_prev, rgb_prev, flow, trunk, rgb, warp, stream=None):
+        n = out.shape[0]
+        self._check(lib().tpmd_stage_tail(self.h, j, _ptr(out), n, _ptr(s_flow), _ptr(flow_prev),
+                                          _ptr(rgb_prev), _ptr(flow), _ptr(trunk), _ptr(rgb),
+                                          _ptr(warp), _stream(stream)))
+
+
+# ---- op level (torch cuda tensors)
+
+def gather(feat, W, H, grid, planar=False, sp=False, out=None, stream=None):
+    """GGML_OP_BILINEAR_GATHER: feat (W*H, C) f32/f16, grid (N, 2) or planar (2, N)."""
+    import torch
+    C = feat.shape[-1]
+    N = grid.numel() // 2
+    if out is None:
+        out = torch.empty((C, N) if sp else (N, C), dtype=torch.float32, device=feat.device)
+    f16 = feat.dtype == torch.float16
+    rc = lib().tpmd_gather(_ptr(feat), int(f16), C, W, H, _ptr(grid), N, int(planar), int(sp),
+                           _ptr(out), _stream(stream))
+    if rc != 0:
+        raise TpmdError("tpmd_gather: invalid arguments")
+    return out
+
+
+def gather_taps(grid, W, H, planar=False, stream=None):
+    import torch
+    N = grid.numel() // 2
+    dev = grid.device
+    x0 = torch.empty(N, dtype=torch.int32, device=dev)
+    y0 = torch.empty(N, dtype=torch.int32, device=dev)
+    wx = torch.empty(N, dtype=torch.float32, device=dev)
+    wy = torch.empty(N, dtype=torch.float32, device=dev)
+    rc = lib().tpmd_gather_taps(_ptr(grid), W, H, N, int(planar), _ptr(x0), _ptr(y0), _ptr(wx),
+                                _ptr(wy), _stream(stream))
+    if rc != 0:
+        raise TpmdError("tpmd_gather_taps: invalid arguments")
+    return x0, y0, wx, wy
+
+
+def upfirdn2x(x, k4, stream=None):
+    import torch
+    H, W = x.shape[-2:]
+    CB = x.numel() // (H * W)
+    y = torch.empty(x.shape[:-2] + (2 * H, 2 * W), dtype=torch.float32, device=x.device)
+    rc = lib().tpmd_upfirdn2x(_ptr(x), _ptr(k4), _ptr(y), W, H, CB, _stream(stream))
+    if rc != 0:
+        raise TpmdError("tpmd_upfirdn2x: invalid arguments")
+    return y
+
+
+def flow_grid(fl, xs, stream=None):
+    import torch
+    N = fl.numel() // 3
+    y = torch.empty((3, N), dtype=torch.float32, device=fl.device)
+    rc = lib().tpmd_flow_grid(_ptr(fl), _ptr(xs), _ptr(y), N, _stream(stream))
+    if rc != 0:
+        raise TpmdError("tpmd_flow_grid: invalid arguments")
+    return y

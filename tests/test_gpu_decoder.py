@@ -1,0 +1,96 @@
+"""Whole-decoder GPU parity through the C ABI against the CPU oracle's fast
+graph (well-conditioned "smooth" workload; see synth.WORKLOADS):
+f32 frames rel-L2 <= 1e-4; f16 frames SSIM >= 0.99 and cosine >= 0.999."""
+import numpy as np
+import pytest
+
+import synth
+import tpmd
+from metrics import cosine, rel_l2, ssim
+
+pytestmark = pytest.mark.gpu
+
+SMALL_IC = (64, 64, 64, 64, 32, 32, 32)
+SMALL_OC = (64, 64, 64, 32, 32, 32, 32)
+
+
+def _decoders(om, ftype, ic, oc, nf, batch, workload="smooth"):
+    raw, lat, feats = synth.workload(workload, nf, ftype, ic, oc)
+    ref = om.Decoder(raw, ftype, ic, oc)
+    ref.set_feats(feats)
+    dec = tpmd.MotionDecoder(ftype, len(ic), ic, oc)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(batch)
+    dec.set_feats(feats)
+    return ref, dec, lat
+
+
+def _frame_ok(ftype, got, want):
+    if ftype == "f32":
+        assert rel_l2(got, want) <= 1e-4, rel_l2(got, want)
+    else:
+        c, s = cosine(got, want), ssim(got, want)
+        assert c >= 0.999 and s >= 0.99, (c, s)
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_decoder_small(om, torch_cuda, ftype):
+    ref, dec, lat = _decoders(om, ftype, SMALL_IC, SMALL_OC, 3, 4)
+    want = ref.decode_fast(lat)
+    got = dec.decode_batch(lat)          # n = 3 < batch = 4
+    assert got.shape == (3, 3, 512, 512)
+    for b in range(3):
+        _frame_ok(ftype, got[b], want[b])
+
+
+@pytest.mark.parametrize("ftype", ["f16", "f32"])
+def test_decoder_reference_channels(om, torch_cuda, ftype):
+    ref, dec, lat = _decoders(om, ftype, synth.REF_IC, synth.REF_OC, 2, 2)
+    want = ref.decode_fast(lat)
+    got = dec.decode_batch(lat)
+    for b in range(2):
+        _frame_ok(ftype, got[b], want[b])
+
+
+def test_decode_paths_agree(om, torch_cuda):
+    """decode (one frame), decode_batch (host) and the device path agree bit
+    for bit, and a frame does not depend on its batch neighbours"""
+    torch = torch_cuda
+    _, dec, lat = _decoders(om, "f16", SMALL_IC, SMALL_OC, 3, 3)
+    full = dec.decode_batch(lat)
+    one = dec.decode(lat[1])
+    assert np.array_equal(one, full[1])
+    part = dec.decode_batch(lat[1:])
+    assert np.array_equal(part, full[1:])
+    sd = torch.from_numpy(lat).cuda()
+    out = torch.empty((3, 3, 512, 512), device="cuda")
+    dec.decode_batch_device(sd, out)
+    dec.sync()
+    assert np.array_equal(out.cpu().numpy(), full)
+
+
+def test_error_contract(torch_cuda):
+    dec = tpmd.MotionDecoder("f32", 2, (64, 64), (64, 64))
+    with pytest.raises(tpmd.TpmdError, match="decoder not prepared"):
+        dec.build(2)
+    with pytest.raises(tpmd.TpmdError, match="missing tensor"):
+        dec.prepare()
+    with pytest.raises(tpmd.TpmdError, match="unknown decoder tensor"):
+        dec.set_weight("dec.nope", np.zeros(4, np.float32))
+    with pytest.raises(tpmd.TpmdError, match="elements"):
+        dec.set_weight("dec.conv1.activate.bias", np.zeros(5, np.float32))
+    raw = synth.raw_weights(1000, "f32", (64, 64), (64, 64))
+    dec.set_weights(raw)
+    dec.prepare()
+    with pytest.raises(tpmd.TpmdError, match="decoder not built"):
+        dec.set_feats(synth.feats(1002, (64, 64)))
+    dec.build(2)
+    with pytest.raises(tpmd.TpmdError, match="feats not set"):
+        dec.decode_batch(np.zeros((1, 512), np.float32))
+    dec.set_feats(synth.feats(1002, (64, 64)))
+    with pytest.raises(tpmd.TpmdError, match="1..2 styles"):
+        dec.decode_batch(np.zeros((3, 512), np.float32))
+    assert tpmd.MotionDecoder.__init__  # constructor rejects bad configs:
+    with pytest.raises(tpmd.TpmdError):
+        tpmd.MotionDecoder("f32", 2, (64, 48), (48, 64))

@@ -1,0 +1,125 @@
+"""Per-stage GPU parity through the C ABI: each decoder stage fed the same
+inputs as the CPU oracle's fast graph.  f32: rel-L2 <= 1e-4 per stage
+output; f16 (f16-in / f32-accumulate): rel-L2 <= 1e-2 and cosine >= 0.9999."""
+import numpy as np
+import pytest
+
+import synth
+import tpmd
+from metrics import cosine, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+SMALL_IC = (64, 64, 64, 64, 32, 32, 32)
+SMALL_OC = (64, 64, 64, 32, 32, 32, 32)
+C1_IC = (512, 512, 512, 512)   # single-stage config: 512 -> 512 at 64x64 is stage 3
+C1_OC = (512, 512, 512, 512)
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def _pair(om, ftype, ic, oc, workload="iid", nf=2):
+    raw, lat, feats = synth.workload(workload, nf, ftype, ic, oc)
+    ref = om.Decoder(raw, ftype, ic, oc)
+    ref.set_feats(feats)
+    dec = tpmd.MotionDecoder(ftype, len(ic), ic, oc)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(nf)
+    dec.set_feats(feats)
+    return ref, dec, lat
+
+
+def _check(ftype, got, want, what):
+    e = rel_l2(got, want)
+    if ftype == "f32":
+        assert e <= 1e-4, (what, e)
+    else:
+        assert e <= 1e-2 and cosine(got, want) >= 0.9999, (what, e, cosine(got, want))
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_modconv_stages_small(om, torch_cuda, ftype):
+    torch = torch_cuda
+    ref, dec, lat = _pair(om, ftype, SMALL_IC, SMALL_OC)
+    g = np.random.default_rng(11)
+    nf = lat.shape[0]
+    # conv1 on the constant input
+    C0 = SMALL_IC[0]
+    s0 = ref.style_of("dec.conv1.conv", lat)
+    want = ref._conv1(s0, ref.demod_den("dec.conv1.conv.weight", s0))
+    x0 = ref.w["dec.input.input"].reshape(C0, 16).T
+    xin = np.ascontiguousarray(np.broadcast_to(x0, (nf, 16, C0)))
+    y = torch.empty((nf, 4, 4, C0), device="cuda")
+    dec.modconv(0, _dev(torch, xin).reshape(nf, 4, 4, C0), _dev(torch, s0), y)
+    _check(ftype, y.cpu().numpy().reshape(nf, 16, C0), want, "conv1")
+    for j in range(len(SMALL_IC)):
+        r = 8 << j
+        IC, OC = SMALL_IC[j], SMALL_OC[j]
+        for L, up in ((1 + 2 * j, True), (2 + 2 * j, False)):
+            base = f"dec.convs.{L - 1}"
+            cin = IC if up else OC
+            H = r // 2 if up else r
+            x = g.standard_normal((nf, H * H, cin)).astype(np.float32)
+            s = ref.style_of(base + ".conv", lat)
+            den = ref.demod_den(base + ".conv.weight", s)
+            if up:
+                want = ref._styled_conv_up_cl(x, H, H, base, s, den)
+            else:
+                want = ref._styled_conv_cl(x, H, H, base, s, den)
+            y = torch.empty((nf, r, r, OC), device="cuda")
+            dec.modconv(L, _dev(torch, x).reshape(nf, H, H, cin), _dev(torch, s), y)
+            _check(ftype, y.cpu().numpy().reshape(nf, r * r, OC), want, base)
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_single_stage_config(om, torch_cuda, ftype):
+    """ModulatedConv2d 512->512 on a 64x64 map with a N(0,1) style, then the
+    ToFlow 1x1 + grid-sample warp of a 512x64x64 feature map"""
+    torch = torch_cuda
+    ref, dec, lat = _pair(om, ftype, C1_IC, C1_OC, nf=1)
+    g = np.random.default_rng(12)
+    x = g.standard_normal((1, 64 * 64, 512)).astype(np.float32)
+    s = g.standard_normal((1, 512)).astype(np.float32)
+    base = "dec.convs.7"
+    want = ref._styled_conv_cl(x, 64, 64, base, s, ref.demod_den(base + ".conv.weight", s))
+    y = torch.empty((1, 64, 64, 512), device="cuda")
+    dec.modconv(8, _dev(torch, x).reshape(1, 64, 64, 512), _dev(torch, s), y)
+    out = y.cpu().numpy().reshape(1, 4096, 512)
+    _check(ftype, out, want, "modconv 512x64x64")
+    # tail on the oracle's conv output (identical input on both sides)
+    fs = ref.style_of("dec.to_flows.3.conv", lat)
+    skf = g.standard_normal((1, 3, 32, 32)).astype(np.float32) * 0.3
+    sk = g.standard_normal((1, 3, 32, 32)).astype(np.float32)
+    fl, warp, trunk, rgb = ref.tail_cl(3, want, fs, skf, sk)
+    t = {k: torch.empty(s_, device="cuda") for k, s_ in
+         (("flow", (1, 3, 64, 64)), ("trunk", (1, 4096, 512)), ("rgb", (1, 3, 64, 64)), ("warp", (1, 4096, 512)))}
+    dec.stage_tail(3, _dev(torch, want), _dev(torch, fs), _dev(torch, skf), _dev(torch, sk),
+                   t["flow"], t["trunk"], t["rgb"], t["warp"])
+    for k, w in (("flow", fl), ("warp", warp), ("trunk", trunk), ("rgb", rgb)):
+        assert rel_l2(t[k].cpu().numpy(), w) <= 1e-4, (k, rel_l2(t[k].cpu().numpy(), w))
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_tail_all_stages_small(om, torch_cuda, ftype):
+    torch = torch_cuda
+    ref, dec, lat = _pair(om, ftype, SMALL_IC, SMALL_OC)
+    g = np.random.default_rng(13)
+    nf = lat.shape[0]
+    skf = sk = None
+    for j in range(len(SMALL_OC)):
+        r, C = 8 << j, SMALL_OC[j]
+        out = g.standard_normal((nf, r * r, C)).astype(np.float32)
+        fs = ref.style_of(f"dec.to_flows.{j}.conv", lat)
+        fl, warp, trunk, rgb = ref.tail_cl(j, out, fs, skf, sk)
+        t = {"flow": torch.empty((nf, 3, r, r), device="cuda"), "trunk": torch.empty((nf, r * r, C), device="cuda"),
+             "rgb": torch.empty((nf, 3, r, r), device="cuda"), "warp": torch.empty((nf, r * r, C), device="cuda")}
+        dec.stage_tail(j, _dev(torch, out), _dev(torch, fs),
+                       None if skf is None else _dev(torch, skf), None if sk is None else _dev(torch, sk),
+                       t["flow"], t["trunk"], t["rgb"], t["warp"])
+        for k, w in (("flow", fl), ("warp", warp), ("trunk", trunk), ("rgb", rgb)):
+            e = rel_l2(t[k].cpu().numpy(), w)
+            assert e <= 1e-4, (j, k, e)
+        skf, sk = fl, rgb
