@@ -119,6 +119,7 @@ def main():
     dec.set_feats(feats)
     lat_dev = torch.from_numpy(np.concatenate([lat, lat[:B]])).cuda()   # wrap-around window
     imgs = torch.empty((B, 3, 512, 512), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()   # inputs resident before the decoder stream reads them
 
     def step(k):
         t0 = (k * B) % n_seq

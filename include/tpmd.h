@@ -103,6 +103,13 @@ int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, in
 int tpmd_decode(tpmd_ctx *ctx, const float *style, float *img);
 /* wait for work enqueued by on_device calls */
 int tpmd_sync(tpmd_ctx *ctx);
+/* enqueue all further work of this context on `stream` (a hipStream_t of
+ * the context's device, e.g. the caller's framework stream; NULL = HIP's
+ * null stream).  A new context uses a non-blocking stream of its own.  No
+ * reference counterpart: ggml owns its stream (src/backend.cpp:169-177);
+ * callers that share device buffers with other stream users need this
+ * ordering. */
+int tpmd_set_stream(tpmd_ctx *ctx, void *stream);
 
 /* Per-stage timing of the next decode_batch: when enabled, the call records
  * HIP events around each launch group and stores microseconds into
@@ -114,7 +121,7 @@ int tpmd_stage_times(const tpmd_ctx *ctx, float *us, int max_slots);
 /* ---- per-stage entry points on DEVICE buffers (f32 in / f32 out) -------
  * These run one piece of the decoder with the context's weights, for
  * parity tests and per-stage measurement.  `stream` is a hipStream_t
- * (NULL = the context stream); they are asynchronous on it. */
+ * (NULL = HIP's null stream); they are asynchronous on it. */
 
 /* ModulatedConv2d with demodulation + FusedLeakyReLU (styled_conv /
  * styled_conv_up / styled_conv_input, src/motion_dec.cpp:357-433):

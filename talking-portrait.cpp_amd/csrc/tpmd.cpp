@@ -75,7 +75,8 @@ struct tpmd_ctx {
     int ns = 7;
     int ic[7] = {}, oc[7] = {};
     std::string err;
-    hipStream_t stream = nullptr;
+    hipStream_t stream = nullptr;     // the stream all work is enqueued on
+    hipStream_t own_stream = nullptr; // created by tpmd_create
 
     std::map<std::string, HostTensor> host;
     bool prepared = false, built = false, feats_set = false;
@@ -178,7 +179,7 @@ struct tpmd_ctx {
         for (void *p : batch_allocs) (void) hipFree(p);
         for (void *p : scr)
             if (p) (void) hipFree(p);
-        if (stream) (void) hipStreamDestroy(stream);
+        if (own_stream) (void) hipStreamDestroy(own_stream);
     }
 };
 
@@ -309,7 +310,8 @@ bool check_ctx(tpmd_ctx *c) {
     return true;
 }
 
-hipStream_t pick_stream(tpmd_ctx *c, void *s) { return s ? (hipStream_t) s : c->stream; }
+// stage entry points run on the caller's stream; NULL is HIP's null stream
+hipStream_t pick_stream(tpmd_ctx *, void *s) { return (hipStream_t) s; }
 
 }  // namespace
 
@@ -362,11 +364,12 @@ tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *st
             return nullptr;
         }
     }
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
         fprintf(stderr, "tpmd_create: stream creation failed\n");
         delete c;
         return nullptr;
     }
+    c->stream = c->own_stream;
     return c;
 }
 
@@ -742,6 +745,12 @@ int tpmd_decode(tpmd_ctx *c, const float *style, float *img) {
     return tpmd_decode_batch(c, style, 1, img, 0);
 }
 
+int tpmd_set_stream(tpmd_ctx *c, void *stream) {
+    if (!check_ctx(c)) return -1;
+    c->stream = (hipStream_t) stream;
+    return 0;
+}
+
 int tpmd_sync(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
     return c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
@@ -841,7 +850,9 @@ int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_
 
 int tpmd_gather(const void *feat, int feat_f16, int C, int W, int H, const float *grid, int64_t N,
                 int planar, int sp, float *dst, void *stream) {
-    if (!feat || !grid || !dst || C < 1 || W < 1 || H < 1 || N < 0) return -1;
+    if (C < 1 || W < 1 || H < 1 || N < 0) return -1;
+    if (N == 0) return 0;  // nothing to sample (empty tensors may carry null pointers)
+    if (!feat || !grid || !dst) return -1;
     return launch_gather(feat, feat_f16 != 0, grid, dst, C, W, H, N, planar, sp, (hipStream_t) stream) ==
                    hipSuccess
                ? 0
@@ -850,7 +861,9 @@ int tpmd_gather(const void *feat, int feat_f16, int C, int W, int H, const float
 
 int tpmd_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0, int32_t *y0,
                      float *wx, float *wy, void *stream) {
-    if (!grid || !x0 || !y0 || !wx || !wy || W < 1 || H < 1 || N < 0) return -1;
+    if (W < 1 || H < 1 || N < 0) return -1;
+    if (N == 0) return 0;
+    if (!grid || !x0 || !y0 || !wx || !wy) return -1;
     return launch_gather_taps(grid, W, H, N, planar, x0, y0, wx, wy, (hipStream_t) stream) == hipSuccess ? 0
                                                                                                       : -1;
 }

@@ -60,6 +60,7 @@ def lib():
             "tpmd_decode_batch": (I, [P, P, I, P, I]),
             "tpmd_decode": (I, [P, P, P]),
             "tpmd_sync": (I, [P]),
+            "tpmd_set_stream": (I, [P, P]),
             "tpmd_profile_stages": (I, [P, I]),
             "tpmd_stage_times": (I, [P, P, I]),
             "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
@@ -97,8 +98,11 @@ def _hptr(a):
 
 
 def _stream(stream):
+    """a hipStream_t for the C ABI: the given torch stream / handle, else
+    torch's current stream (so launches are ordered with torch's copies)"""
     if stream is None:
-        return None
+        import torch
+        stream = torch.cuda.current_stream()
     return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
 
 
@@ -194,6 +198,11 @@ class MotionDecoder:
 
     def sync(self):
         self._check(lib().tpmd_sync(self.h))
+
+    def use_stream(self, stream=None):
+        """enqueue the decoder's work on `stream` (torch stream or handle;
+        None = torch's current stream)"""
+        self._check(lib().tpmd_set_stream(self.h, _stream(stream)))
 
     def profile_stages(self, enable=True):
         return lib().tpmd_profile_stages(self.h, 1 if enable else 0)

@@ -65,6 +65,7 @@ def test_decode_paths_agree(om, torch_cuda):
     assert np.array_equal(part, full[1:])
     sd = torch.from_numpy(lat).cuda()
     out = torch.empty((3, 3, 512, 512), device="cuda")
+    dec.use_stream()                     # order the decode after torch's copy
     dec.decode_batch_device(sd, out)
     dec.sync()
     assert np.array_equal(out.cpu().numpy(), full)
