@@ -71,6 +71,14 @@ const char *tpmd_last_error(const tpmd_ctx *ctx);
  * stored f16 (src/gguf_load.cpp:149-153).  n = element count (checked). */
 int tpmd_set_weight(tpmd_ctx *ctx, const char *name, const float *data, int64_t n, int flags);
 
+/* The decoder tensors this context expects, i = 0, 1, ...: GGUF name,
+ * element count and whether the tensor is a 2-D-or-larger weight (stored
+ * f16 in an f16 GGUF).  Returns the name, or NULL past the last tensor.
+ * Replaces the weight list the reference walks implicitly through
+ * weights_t lookups (src/motion_dec.cpp:249-261) and motion_dec_host_tensors
+ * (src/motion_dec.cpp:17-29). */
+const char *tpmd_weight_name(const tpmd_ctx *ctx, int i, int64_t *n, int *is_matrix);
+
 /* motion_dec::prepare (src/motion_dec.h:38, src/motion_dec.cpp:31-226):
  * S_aug demodulation Gram rows, composed sub-pixel up-conv kernels, cf GEMM
  * matrices; uploads every derived tensor.  Fails naming the first missing

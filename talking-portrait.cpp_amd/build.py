@@ -28,7 +28,11 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", 
              "-munsafe-fp-atomics"]
 
 SOURCES = ["k_gather.hip", "k_conv.hip", "k_tail.hip", "k_style.hip", "tpmd.cpp"]
+# plain C++ over the C ABI (no HIP): the tp::motion_dec shim, in the library
 HOST_SOURCES = ["motion_dec.cpp"]
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOSTDIR}"]
+SHIM_CHECK = os.path.join(PKG, "shim_check")
 
 
 def _run(cmd):
@@ -51,9 +55,8 @@ def build(verbose=False):
         jobs.append([HIPCC, *COMMON, *HIP_FLAGS, "-x", "hip", "-c", src, "-o", obj])
     for s in HOST_SOURCES:
         src = os.path.join(HOSTDIR, s)
-        if os.path.exists(src):
-            obj = os.path.join(BUILD, "host_" + s + ".o")
-            jobs.append([HIPCC, *COMMON, *HIP_FLAGS, "-x", "hip", "-c", src, "-o", obj])
+        obj = os.path.join(BUILD, "host_" + s + ".o")
+        jobs.append([CXX, *HOST_FLAGS, "-c", src, "-o", obj])
     objs = [j[-1] for j in jobs]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for out in ex.map(_run, jobs):
@@ -62,6 +65,11 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
+    # the shim's driver, linked against the library next to it
+    tmp = SHIM_CHECK + ".tmp"
+    _run([CXX, *HOST_FLAGS, os.path.join(HOSTDIR, "shim_check.cpp"), "-o", tmp, f"-L{PKG}", "-ltpmd",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, SHIM_CHECK)
     return LIB
 
 

@@ -79,6 +79,7 @@ struct tpmd_ctx {
     hipStream_t own_stream = nullptr; // created by tpmd_create
 
     std::map<std::string, HostTensor> host;
+    std::vector<std::pair<std::string, std::vector<int64_t>>> tensors;  // expected inputs
     bool prepared = false, built = false, feats_set = false;
     std::vector<void *> allocs;      // weights / constants
     std::vector<void *> batch_allocs;
@@ -204,36 +205,47 @@ double motion_ae_scale(const std::string &name, const std::vector<int64_t> &ne) 
     return 1.0;
 }
 
-// expected torch shape of every decoder tensor for this config (Appendix of
-// the GGUF layout: src/motion_dec.cpp:17-29, tests/test_gguf.cpp:54-58)
-bool expected_shape(const tpmd_ctx *c, const std::string &name, std::vector<int64_t> &shape) {
-    const int C0 = c->ic[0];
-    auto is = [&](const std::string &s) { return name == s; };
-    if (is("dec.input.input")) { shape = {1, C0, 4, 4}; return true; }
-    if (is("dec.conv1.conv.weight")) { shape = {1, C0, C0, 3, 3}; return true; }
-    if (is("dec.conv1.conv.modulation.weight")) { shape = {C0, 512}; return true; }
-    if (is("dec.conv1.conv.modulation.bias") || is("dec.conv1.activate.bias")) { shape = {C0}; return true; }
-    for (int i = 0; i < 2 * c->ns; i++) {
-        const int j = i / 2;
-        const int cin = (i % 2 == 0) ? c->ic[j] : c->oc[j], cout = c->oc[j];
-        const std::string b = fmt("dec.convs.%d", i);
-        if (is(b + ".conv.weight")) { shape = {1, cout, cin, 3, 3}; return true; }
-        if (is(b + ".conv.modulation.weight")) { shape = {cin, 512}; return true; }
-        if (is(b + ".conv.modulation.bias")) { shape = {cin}; return true; }
-        if (is(b + ".activate.bias")) { shape = {cout}; return true; }
-        if (i % 2 == 0 && is(b + ".conv.blur.kernel")) { shape = {4, 4}; return true; }
-    }
+// every decoder tensor of this config with its torch shape, in GGUF names
+// (src/motion_dec.cpp:17-29, :249-261; shapes as tests/test_gguf.cpp:54-58)
+std::vector<std::pair<std::string, std::vector<int64_t>>> tensor_list(const tpmd_ctx *c) {
+    std::vector<std::pair<std::string, std::vector<int64_t>>> v;
+    const int64_t C0 = c->ic[0];
+    v.push_back({"dec.input.input", {1, C0, 4, 4}});
+    v.push_back({"dec.conv1.conv.weight", {1, C0, C0, 3, 3}});
+    v.push_back({"dec.conv1.conv.modulation.weight", {C0, 512}});
+    v.push_back({"dec.conv1.conv.modulation.bias", {C0}});
+    v.push_back({"dec.conv1.activate.bias", {C0}});
     for (int j = 0; j < c->ns; j++) {
-        const int C = c->oc[j];
+        for (int i = 2 * j; i <= 2 * j + 1; i++) {
+            const int64_t cin = (i % 2 == 0) ? c->ic[j] : c->oc[j], cout = c->oc[j];
+            const std::string b = fmt("dec.convs.%d", i);
+            v.push_back({b + ".conv.weight", {1, cout, cin, 3, 3}});
+            v.push_back({b + ".conv.modulation.weight", {cin, 512}});
+            v.push_back({b + ".conv.modulation.bias", {cin}});
+            v.push_back({b + ".activate.bias", {cout}});
+            if (i % 2 == 0) v.push_back({b + ".conv.blur.kernel", {4, 4}});
+        }
+        const int64_t C = c->oc[j];
         const std::string f = fmt("dec.to_flows.%d", j), r = fmt("dec.to_rgbs.%d", j);
-        if (is(f + ".conv.weight")) { shape = {1, 3, C, 1, 1}; return true; }
-        if (is(f + ".conv.modulation.weight")) { shape = {C, 512}; return true; }
-        if (is(f + ".conv.modulation.bias")) { shape = {C}; return true; }
-        if (is(f + ".bias") || is(r + ".bias")) { shape = {1, 3, 1, 1}; return true; }
-        if (is(f + ".upsample.kernel") || is(r + ".upsample.kernel")) { shape = {4, 4}; return true; }
-        if (is(r + ".conv.0.weight")) { shape = {3, C, 1, 1}; return true; }
-        if (is(r + ".conv.1.bias")) { shape = {3}; return true; }
+        v.push_back({f + ".conv.weight", {1, 3, C, 1, 1}});
+        v.push_back({f + ".conv.modulation.weight", {C, 512}});
+        v.push_back({f + ".conv.modulation.bias", {C}});
+        v.push_back({f + ".bias", {1, 3, 1, 1}});
+        v.push_back({f + ".upsample.kernel", {4, 4}});
+        v.push_back({r + ".conv.0.weight", {3, C, 1, 1}});
+        v.push_back({r + ".conv.1.bias", {3}});
+        v.push_back({r + ".bias", {1, 3, 1, 1}});
+        v.push_back({r + ".upsample.kernel", {4, 4}});
     }
+    return v;
+}
+
+bool expected_shape(const tpmd_ctx *c, const std::string &name, std::vector<int64_t> &shape) {
+    for (const auto &t : c->tensors)
+        if (t.first == name) {
+            shape = t.second;
+            return true;
+        }
     return false;
 }
 
@@ -364,6 +376,7 @@ tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *st
             return nullptr;
         }
     }
+    c->tensors = tensor_list(c);
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
         fprintf(stderr, "tpmd_create: stream creation failed\n");
         delete c;
@@ -412,6 +425,16 @@ int tpmd_set_weight(tpmd_ctx *c, const char *name, const float *data, int64_t n,
     c->host[name] = std::move(t);
     c->prepared = false;
     return 0;
+}
+
+const char *tpmd_weight_name(const tpmd_ctx *c, int i, int64_t *n, int *is_matrix) {
+    if (!c || i < 0 || i >= (int) c->tensors.size()) return nullptr;
+    const auto &t = c->tensors[(size_t) i];
+    int64_t e = 1;
+    for (auto d : t.second) e *= d;
+    if (n) *n = e;
+    if (is_matrix) *is_matrix = t.second.size() >= 2 ? 1 : 0;
+    return t.first.c_str();
 }
 
 int tpmd_prepare(tpmd_ctx *c) {

@@ -1,0 +1,168 @@
+// shim_check — drives tp::motion_dec (host/motion_dec.h) the way the
+// reference's generation loop does (src/pipeline.cpp:153-185): prepare,
+// build, set_feats, then decode_batch over a clip in `batch`-frame launches
+// with the tail padded by repeating the last frame, plus one single-frame
+// decode().  Inputs come from a little-endian blob file:
+//
+//   "TPMDBLOB" u32 n_stages, i32 ic[n], i32 oc[n], u32 ftype_f16,
+//   u32 n_tensors, { u32 len, name, u8 f16_in_file, u64 n, f32 data[n] }...,
+//   feats j < n_stages: f32 [r_j*r_j*OC_j],
+//   u32 n_frames, f32 styles[n_frames][512]
+//
+// Output file: f32 frames [n_frames][3][R][R], then the single-frame decode
+// of frame 0 [3][R][R].  Exit status 0 on success; errors on stderr.
+//
+//   shim_check <blob> <out> [device]
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "motion_dec.h"
+
+namespace {
+
+struct reader {
+    std::vector<uint8_t> b;
+    size_t p = 0;
+    bool ok = true;
+    template <typename T>
+    T get() {
+        T v{};
+        if (p + sizeof(T) > b.size()) {
+            ok = false;
+            return v;
+        }
+        memcpy(&v, b.data() + p, sizeof(T));
+        p += sizeof(T);
+        return v;
+    }
+    bool bytes(void *dst, size_t n) {
+        if (p + n > b.size()) return ok = false;
+        memcpy(dst, b.data() + p, n);
+        p += n;
+        return true;
+    }
+};
+
+struct blob_weights : tp::weight_source {
+    struct t {
+        std::vector<float> v;
+        bool f16;
+    };
+    std::map<std::string, t> m;
+    bool get(const std::string &name, std::vector<float> &data, bool &f16) const override {
+        auto it = m.find(name);
+        if (it == m.end()) return false;
+        data = it->second.v;
+        f16 = it->second.f16;
+        return true;
+    }
+};
+
+struct menc_like {  // the member of menc_result that set_feats reads
+    std::vector<std::vector<float>> feats;
+};
+
+struct no_taps {
+    explicit operator bool() const { return false; }
+};
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc < 3) {
+        fprintf(stderr, "usage: shim_check <blob> <out> [device]\n");
+        return 2;
+    }
+    reader r;
+    {
+        FILE *f = fopen(argv[1], "rb");
+        if (!f) {
+            fprintf(stderr, "cannot open %s\n", argv[1]);
+            return 1;
+        }
+        fseek(f, 0, SEEK_END);
+        r.b.resize((size_t) ftell(f));
+        fseek(f, 0, SEEK_SET);
+        if (fread(r.b.data(), 1, r.b.size(), f) != r.b.size()) r.ok = false;
+        fclose(f);
+    }
+    char magic[8];
+    if (!r.bytes(magic, 8) || memcmp(magic, "TPMDBLOB", 8) != 0) {
+        fprintf(stderr, "bad blob\n");
+        return 1;
+    }
+    tp::hip_backend be;
+    be.device = argc > 3 ? atoi(argv[3]) : 0;
+    be.n_stages = (int) r.get<uint32_t>();
+    if (be.n_stages < 1 || be.n_stages > 7) return 1;
+    be.stage_ic.resize((size_t) be.n_stages);
+    be.stage_oc.resize((size_t) be.n_stages);
+    for (auto &v : be.stage_ic) v = r.get<int32_t>();
+    for (auto &v : be.stage_oc) v = r.get<int32_t>();
+    be.ftype = r.get<uint32_t>() ? "f16" : "f32";
+    blob_weights w;
+    const uint32_t nt = r.get<uint32_t>();
+    for (uint32_t i = 0; i < nt && r.ok; i++) {
+        std::string name(r.get<uint32_t>(), '\0');
+        r.bytes(&name[0], name.size());
+        blob_weights::t t;
+        t.f16 = r.get<uint8_t>() != 0;
+        t.v.resize(r.get<uint64_t>());
+        r.bytes(t.v.data(), t.v.size() * 4);
+        w.m[name] = std::move(t);
+    }
+    menc_like m;
+    for (int j = 0; j < be.n_stages; j++) {
+        const size_t r2 = (size_t) (8 << j) * (8 << j);
+        m.feats.emplace_back(r2 * (size_t) be.stage_oc[(size_t) j]);
+        r.bytes(m.feats.back().data(), m.feats.back().size() * 4);
+    }
+    const uint32_t nf = r.get<uint32_t>();
+    std::vector<float> styles((size_t) nf * 512);
+    r.bytes(styles.data(), styles.size() * 4);
+    if (!r.ok || nf == 0) {
+        fprintf(stderr, "truncated blob\n");
+        return 1;
+    }
+
+    tp::motion_dec dec;
+    dec.w = &w;
+    std::string err;
+    if (!dec.prepare(be, err) || !dec.build(be, false, err) || !dec.set_feats(m, err)) {
+        fprintf(stderr, "shim_check: %s\n", err.c_str());
+        return 1;
+    }
+    const int BQ = dec.batch;
+    const size_t fsz = (size_t) 3 * dec.res * dec.res;
+    std::vector<float> out((size_t) nf * fsz + fsz), bst((size_t) BQ * 512), bimg((size_t) BQ * fsz);
+    for (uint32_t t0 = 0; t0 < nf; t0 += (uint32_t) BQ) {
+        for (int b = 0; b < BQ; b++) {
+            const uint32_t t = t0 + (uint32_t) b < nf ? t0 + (uint32_t) b : nf - 1;
+            memcpy(bst.data() + (size_t) b * 512, styles.data() + (size_t) t * 512, 512 * 4);
+        }
+        if (!dec.decode_batch(be, bst.data(), bimg.data(), err)) {
+            fprintf(stderr, "shim_check: %s\n", err.c_str());
+            return 1;
+        }
+        const uint32_t nb = nf - t0 < (uint32_t) BQ ? nf - t0 : (uint32_t) BQ;
+        memcpy(out.data() + (size_t) t0 * fsz, bimg.data(), (size_t) nb * fsz * 4);
+    }
+    no_taps tap;
+    if (!dec.decode(be, styles.data(), out.data() + (size_t) nf * fsz, tap, err)) {
+        fprintf(stderr, "shim_check: %s\n", err.c_str());
+        return 1;
+    }
+    FILE *f = fopen(argv[2], "wb");
+    if (!f || fwrite(out.data(), 4, out.size(), f) != out.size()) {
+        fprintf(stderr, "cannot write %s\n", argv[2]);
+        return 1;
+    }
+    fclose(f);
+    printf("shim_check: %u frames in batches of %d, %d stages, ftype %s\n", nf, BQ, be.n_stages,
+           be.ftype.c_str());
+    return 0;
+}

@@ -51,6 +51,7 @@ def lib():
             "tpmd_destroy": (None, [P]),
             "tpmd_last_error": (C, [P]),
             "tpmd_set_weight": (I, [P, C, P, I64, I]),
+            "tpmd_weight_name": (C, [P, I, P, P]),
             "tpmd_prepare": (I, [P]),
             "tpmd_build": (I, [P, I]),
             "tpmd_batch": (I, [P]),
@@ -154,6 +155,18 @@ class MotionDecoder:
         a = np.ascontiguousarray(arr, dtype=np.float32)
         flags = (W_F16_FILE if f16_file else 0) | (W_FOLDED if folded else 0)
         self._check(lib().tpmd_set_weight(self.h, name.encode(), _hptr(a), a.size, flags))
+
+    def weight_names(self):
+        """(name, element count, is_matrix) of every tensor this context expects"""
+        out = []
+        n, m = ctypes.c_int64(), ctypes.c_int()
+        i = 0
+        while True:
+            nm = lib().tpmd_weight_name(self.h, i, ctypes.byref(n), ctypes.byref(m))
+            if nm is None:
+                return out
+            out.append((nm.decode(), n.value, bool(m.value)))
+            i += 1
 
     def set_weights(self, raw):
         for name, (arr, f16) in raw.items():

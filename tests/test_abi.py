@@ -18,3 +18,12 @@ def test_abi_version_and_null_safety():
     assert L.tpmd_abi_version() == 1
     assert L.tpmd_last_error(None) == b"no context"
     L.tpmd_destroy(None)
+
+
+def test_shim_driver_is_built():
+    """the tp::motion_dec driver links against the library (usage error, no GPU use)"""
+    import os
+    import subprocess
+    shim = os.path.join(os.path.dirname(tpmd.LIB_PATH), "shim_check")
+    p = subprocess.run([shim], capture_output=True, text=True, timeout=60)
+    assert p.returncode == 2 and "usage" in p.stderr

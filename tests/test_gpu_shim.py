@@ -1,0 +1,70 @@
+"""The C++ tp::motion_dec shim (host/motion_dec.h), driven like the
+reference's generation loop (src/pipeline.cpp:153-185) by host/shim_check:
+its frames equal the Python binding's bit for bit (same library, same
+kernels), its single-frame decode() equals decode_batch's frame, and the
+tensor list it walks matches the synthetic checkpoint's names."""
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import synth
+import tpmd
+
+pytestmark = pytest.mark.gpu
+
+IC = (64, 64, 64, 32, 32, 32, 32)
+OC = (64, 64, 32, 32, 32, 32, 32)
+SHIM = os.path.join(os.path.dirname(tpmd.LIB_PATH), "shim_check")
+
+
+def write_blob(path, raw, feats, styles, ic, oc, f16):
+    with open(path, "wb") as f:
+        f.write(b"TPMDBLOB")
+        f.write(struct.pack("<I", len(ic)))
+        f.write(struct.pack(f"<{len(ic)}i", *ic))
+        f.write(struct.pack(f"<{len(oc)}i", *oc))
+        f.write(struct.pack("<II", int(f16), len(raw)))
+        for name, (arr, f16_file) in raw.items():
+            nb = name.encode()
+            a = np.ascontiguousarray(arr, np.float32).ravel()
+            f.write(struct.pack("<I", len(nb)) + nb + struct.pack("<BQ", int(f16_file), a.size))
+            f.write(a.tobytes())
+        for x in feats:
+            f.write(np.ascontiguousarray(x, np.float32).tobytes())
+        f.write(struct.pack("<I", styles.shape[0]))
+        f.write(np.ascontiguousarray(styles, np.float32).tobytes())
+
+
+@pytest.mark.parametrize("ftype", ["f16", "f32"])
+def test_shim_matches_binding(torch_cuda, tmp_path, ftype):
+    raw, lat, feats = synth.workload("smooth", 5, ftype, IC, OC)
+    blob, out = tmp_path / "in.blob", tmp_path / "out.f32"
+    write_blob(blob, raw, feats, lat, IC, OC, ftype == "f16")
+    env = dict(os.environ, TP_MDEC_BATCH="2")      # 3 launches, the last one padded
+    p = subprocess.run([SHIM, str(blob), str(out)], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode == 0, p.stderr
+    R = 512
+    got = np.fromfile(out, np.float32).reshape(6, 3, R, R)
+    dec = tpmd.MotionDecoder(ftype, len(IC), IC, OC)
+    assert sorted(n for n, _, _ in dec.weight_names()) == sorted(raw)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(2)
+    dec.set_feats(feats)
+    want = np.concatenate([dec.decode_batch(lat[t:t + 2]) for t in range(0, 5, 2)])
+    assert np.array_equal(got[:5], want)
+    assert np.array_equal(got[5], want[0])
+
+
+def test_shim_errors(torch_cuda, tmp_path):
+    raw, lat, feats = synth.workload("smooth", 1, "f32", IC, OC)
+    del raw["dec.to_rgbs.3.bias"]
+    blob = tmp_path / "in.blob"
+    write_blob(blob, raw, feats, lat, IC, OC, False)
+    p = subprocess.run([SHIM, str(blob), str(tmp_path / "o")], capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode == 1 and "missing tensor dec.to_rgbs.3.bias" in p.stderr
