@@ -24,9 +24,15 @@ PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}
 REF_FPS_RTX5070TI = 213.2   # mdec, GGML-CUDA f16 fast graph (docs/vulkan-perf.md:134,143)
 
 
+def fused_tail(oc):
+    """stages whose dense conv runs the stage tail in its epilogue"""
+    return oc in (32, 64, 128)
+
+
 def stage_costs(ic, oc, nframes, ftype):
-    """algorithmic FLOPs and HBM bytes of every profiled launch group of one
-    decode_batch call (slot order of tpmd_stage_times)"""
+    """(name, algorithmic FLOPs, algorithmic HBM bytes) of every profiled
+    launch group of one decode_batch call, in tpmd_stage_times slot order;
+    None for the empty tail slot of a fused stage"""
     sa = 2 if ftype == "f16" else 4   # conv operand / activation bytes
     sw = sa                            # conv weight bytes
     C0 = ic[0]
@@ -39,17 +45,21 @@ def stage_costs(ic, oc, nframes, ftype):
         r = 8 << j
         IC, OC = ic[j], oc[j]
         last = j + 1 == len(ic)
-        f_up = 2 * nframes * r * r * 9 * IC * OC
-        b_up = nframes * (r // 2) ** 2 * IC * sa + nframes * r * r * OC * sa + 4 * OC * 9 * IC * sw
-        f_dn = 2 * nframes * r * r * 9 * OC * OC
-        b_dn = nframes * r * r * OC * sa + nframes * r * r * OC * 4 + 9 * OC * OC * sw
-        # tail: read out (f32) + feats once + prev skips; write trunk, flow, rgb
-        b_tl = (nframes * r * r * OC * 4 + r * r * OC * sa
-                + (nframes * 2 * 3 * (r // 2) ** 2 * 4 if j else 0)
-                + (0 if last else nframes * r * r * OC * sa + nframes * 3 * r * r * 4)
-                + nframes * 3 * r * r * 4)
-        f_tl = nframes * r * r * OC * 2 * 6
-        slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv", f_dn, b_dn), (f"r{r}.tail", f_tl, b_tl)]
+        px = nframes * r * r
+        f_up = 2 * px * 9 * IC * OC
+        b_up = nframes * (r // 2) ** 2 * IC * sa + px * OC * sa + 4 * OC * 9 * IC * sw
+        f_dn = 2 * px * 9 * OC * OC
+        # tail: feats once, previous skips, trunk (next operand), flow and rgb
+        b_tl = (r * r * OC * sa + (nframes * 2 * 3 * (r // 2) ** 2 * 4 if j else 0)
+                + (0 if last else px * OC * sa + px * 3 * 4) + px * 3 * 4)
+        f_tl = px * OC * 2 * 6
+        if fused_tail(OC):
+            b_dt = px * OC * sa + 9 * OC * OC * sw + b_tl
+            slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv+tail", f_dn + f_tl, b_dt), None]
+        else:
+            b_dn = px * OC * sa + px * OC * 4 + 9 * OC * OC * sw
+            slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv", f_dn, b_dn),
+                      (f"r{r}.tail", f_tl, b_tl + px * OC * 4)]
     return slots
 
 
@@ -147,7 +157,7 @@ def main():
     dec.profile_stages(False)
     us = acc / nprof
     slots = stage_costs(dec.ic, dec.oc, B, args.ftype)
-    stages = [roofline(n, f, b, u, args.ftype) for (n, f, b), u in zip(slots, us)]
+    stages = [roofline(sl[0], sl[1], sl[2], u, args.ftype) for sl, u in zip(slots, us) if sl is not None]
     dom = max(range(len(stages)), key=lambda i: stages[i]["us"])
     r = dict(stages[dom])
     r["kernel"] = r.pop("name")

@@ -122,7 +122,9 @@ int tpmd_set_stream(tpmd_ctx *ctx, void *stream);
 /* Per-stage timing of the next decode_batch: when enabled, the call records
  * HIP events around each launch group and stores microseconds into
  * us[0..n_slots) (slot 0 = style + demod + conv1, then 3 per stage: up-conv,
- * dense conv, tail).  Returns the slot count, or -1. */
+ * dense conv, tail; stages with OC <= 128 run the tail inside the dense conv,
+ * so their dense slot holds both and their tail slot is empty).  Returns the
+ * slot count, or -1. */
 int tpmd_profile_stages(tpmd_ctx *ctx, int enable);
 int tpmd_stage_times(const tpmd_ctx *ctx, float *us, int max_slots);
 
@@ -148,6 +150,15 @@ int tpmd_modconv(tpmd_ctx *ctx, int conv, const float *x, int n, int H, int W, c
 int tpmd_stage_tail(tpmd_ctx *ctx, int j, const float *out, int n, const float *s_flow,
                     const float *flow_prev, const float *rgb_prev, float *flow, float *trunk,
                     float *rgb, float *warp, void *stream);
+
+/* Dense conv of stage j followed by the stage tail, exactly as decode runs
+ * them (fused into one kernel when OC_j <= 128, src/motion_dec.cpp:357-373
+ * then :1077-1108): c1: CL [n][r][r][OC_j] f32 up-conv output (before this
+ * conv's modulation); s_conv: [n][OC_j] this conv's style (demodulation
+ * computed from it); other arguments as tpmd_stage_tail, trunk CL f32. */
+int tpmd_stage_conv_tail(tpmd_ctx *ctx, int j, const float *c1, int n, const float *s_conv,
+                         const float *s_flow, const float *flow_prev, const float *rgb_prev,
+                         float *flow, float *trunk, float *rgb, float *warp, void *stream);
 
 /* ---- op-level entry points (no context) ------------------------------- */
 

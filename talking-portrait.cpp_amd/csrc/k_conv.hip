@@ -16,31 +16,61 @@
 //   X(k, n) = x[frame][y+kh-1][x+kw-1][ic], zero outside the map.
 // Style modulation is applied to the input activation by its producer (the
 // stored activation is x * s for this conv), so A is shared by every frame of
-// the batch and streamed once per tile row; demodulation (1/den), the
-// FusedLeakyReLU bias + leaky and the NEXT conv's style are fused into the
-// epilogue.
+// the batch; demodulation (1/den), the FusedLeakyReLU bias + leaky and the
+// NEXT conv's style are applied in the epilogue.
 //
-// Tiling: BM x BN block tile, BK-wide k tiles staged through LDS
-// (double-buffered, 16-byte rows padded to 144 B so every 32x32 MFMA operand
-// read is one bank-conflict-free ds_read_b128), WM x WN waves each owning a
-// (BM/WM) x (BN/WN) tile of 32x32 MFMA accumulators.
+// Tiling: a BM x BN block tile per workgroup, k tiles of RB bytes per row
+// staged through double-buffered LDS (rows padded by 16 bytes so every
+// 32x32 MFMA operand read is a conflict-free ds_read_b128), WM x WN waves
+// each owning (BM/WM) x (BN/WN) of 32x32 MFMA accumulators.  One barrier per
+// k tile: the next tile's global loads are in flight while the current one
+// is multiplied.
 //   f16: v_mfma_f32_32x32x16_f16 (f16 in, f32 accumulate)
 //   f32: v_mfma_f32_32x32x2_f32, four per 16-byte operand read; the lane's k
 //        assignment is a permutation shared by A and B, so every product pairs
 //        A[m][k] with X(k, n) exactly once.
-#include "tpmd_device.h"
-#include "tpmd_launch.h"
+// Tile order: workgroup ids are renumbered so that each of the 8 XCDs (which
+// receive ids round robin) works on a contiguous range of tiles, M fastest,
+// so the B tile of a pixel block stays in that XCD's L2 for all its M tiles.
+//
+// Epilogues:
+//   EPI_STORE  : 1/den, bias, leaky, * next style, store (sub-pixel: to the
+//                interleaved output pixel)
+//   EPI_PARTIAL: split-K — raw f32 partial sums to a workspace
+//                [split][N][M]; splitk_reduce_kernel adds the splits in a
+//                fixed order and applies the EPI_STORE epilogue
+//   EPI_TAIL   : dense convs whose tile holds every channel (OC <= 128): the
+//                activated tile goes to LDS as f32 and the stage tail
+//                (tpmd_tail.h) runs on it, so the stage output never reaches
+//                HBM.
+#include <utility>
+
+#include "tpmd_tail.h"
 
 namespace tpmd {
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>): compile-time
+// indices, so register arrays indexed inside never go to scratch
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 enum { MODE_DENSE = 0, MODE_SUBPIX = 1 };
+enum { EPI_STORE = 0, EPI_PARTIAL = 1, EPI_TAIL = 2 };
 
 template <typename TA>
 struct mfma_op;
 
 template <>
 struct mfma_op<half_t> {
-    __device__ __forceinline__ static void run(const uint4 &a, const uint4 &b, floatx16 &c) {
+    __device__ __forceinline__ static void run(const u32x4 &a, const u32x4 &b, floatx16 &c) {
         c = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *) &a, *(const half8 *) &b, c, 0, 0,
                                                    0);
     }
@@ -48,7 +78,7 @@ struct mfma_op<half_t> {
 
 template <>
 struct mfma_op<float> {
-    __device__ __forceinline__ static void run(const uint4 &a, const uint4 &b, floatx16 &c) {
+    __device__ __forceinline__ static void run(const u32x4 &a, const u32x4 &b, floatx16 &c) {
         const floatx4 av = *(const floatx4 *) &a, bv = *(const floatx4 *) &b;
         c = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], bv[0], c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], bv[1], c, 0, 0, 0);
@@ -65,97 +95,162 @@ template <> __device__ __forceinline__ void store4<half_t>(half_t *p, float a, f
     *(half4 *) p = half4{(half_t) a, (half_t) b, (half_t) c, (half_t) d};
 }
 
-// RB: bytes of one k tile row (128 or 64); BK = RB / sizeof(act) must divide IC
-template <typename TA, typename TO, int BM, int BN, int WM, int WN, int MODE, int RB>
-__global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(
-    const TA *__restrict__ A,        // [M][9*IC]
-    const TA *__restrict__ X,        // CL input, frame stride x_bstride elements
-    TO *__restrict__ Y,              // CL output
-    const float *__restrict__ inv_den,   // [B][OC]
-    const float *__restrict__ bias,      // [OC]
-    const float *__restrict__ out_scale, // [B][OC] or null
-    int N, int H, int W, int IC, int OC, int64_t x_bstride) {
+struct ConvParams {
+    const void *A;          // [M][9*IC]
+    const void *X;          // CL input, frame stride x_bstride elements
+    void *Y;                // CL output (EPI_STORE)
+    const float *inv_den;   // [frame][OC]
+    const float *bias;      // [OC]
+    const float *out_scale; // [frame][OC] or null
+    float *ws;              // [split][N][M] (EPI_PARTIAL)
+    int N, H, W, IC, OC, M;
+    int MT;                 // M tiles
+    int T;                  // k tiles (9 * IC / BK)
+    int64_t x_bstride;
+};
+
+// hardware hands workgroup ids to the 8 XCDs round robin; renumber so each
+// XCD processes a contiguous range of `total` tiles
+__device__ __forceinline__ int xcd_remap(int L, int total) {
+    const int per = total >> 3, rem = total & 7;
+    const int xcd = L & 7, slot = L >> 3;
+    return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+// activation of 4 consecutive GEMM rows m..m+3 of column n, stored to Y
+template <typename TO, int MODE>
+__device__ __forceinline__ void epi_store_quad(const ConvParams &p, const float acc[4], int m, int n) {
+    const int HW = p.H * p.W;
+    const int fr = n / HW;
+    int o;
+    int64_t opix;
+    if (MODE == MODE_DENSE) {
+        o = m;
+        opix = n;
+    } else {
+        const int rem = n - fr * HW;
+        const int y = rem / p.W, x = rem - y * p.W;
+        const int cls = m / p.OC;
+        o = m - cls * p.OC;
+        opix = (int64_t) fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * p.W) + 2 * x + (cls & 1);
+    }
+    const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + o);
+    const floatx4 bb = *(const floatx4 *) (p.bias + o);
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = leaky(acc[j] * id[j] + bb[j]);
+    if (p.out_scale) {
+        const floatx4 sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] *= sc[j];
+    }
+    store4<TO>((TO *) p.Y + opix * p.OC + o, v[0], v[1], v[2], v[3]);
+}
+
+template <int BM, int BN, int RB, int EPI>
+struct conv_lds {
+    static constexpr int RS = RB + 16;                  // padded row stride (bytes)
+    static constexpr int BUF = (BM + BN) * RS;
+    static constexpr int KLOOP = 2 * BUF;
+    static constexpr int TAIL = EPI == EPI_TAIL ? BN * (BM + 4) * 4 : 0;
+    static constexpr int BYTES = KLOOP > TAIL ? KLOOP : TAIL;
+};
+
+template <typename TA, typename TO, int BM, int BN, int WM, int WN, int RB, int MODE, int EPI,
+          typename TF, typename TT>
+__global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, TailArgs ta) {
     constexpr int NT = WM * WN * 64;
-    constexpr int kRowBytes = RB;
-    constexpr int kRowStride = RB + 16;           // padded LDS row (bytes)
-    constexpr int BK = RB / (int) sizeof(TA);     // elements per k tile
-    constexpr int VEC = 16 / sizeof(TA);          // elements per 16-byte chunk
-    constexpr int CR = kRowBytes / 16;            // chunks per LDS row
-    constexpr int A_PER = (BM * CR + NT - 1) / NT;  // A chunks per thread
-    constexpr int B_PER = (BN * CR + NT - 1) / NT;  // B chunks per thread
-    constexpr bool A_PART = BM * CR < NT;         // only the first BM*CR threads load A
-    constexpr bool B_PART = BN * CR < NT;
-    constexpr int ROWS_PER_PASS = NT / CR;
+    constexpr int RS = RB + 16;
+    constexpr int BK = RB / (int) sizeof(TA);       // elements per k tile row
+    constexpr int VEC = 16 / (int) sizeof(TA);      // elements per 16-byte chunk
+    constexpr int CR = RB / 16;                      // chunks per row
+    constexpr int A_CH = BM * CR, B_CH = BN * CR;
+    constexpr bool A_PART = A_CH < NT;               // only the first A_CH threads load A
+    constexpr int A_PER = A_PART ? 1 : A_CH / NT;
+    constexpr int B_PER = B_CH / NT;
+    constexpr int RPP = NT / CR;                     // rows per loader pass
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    static_assert((BM * CR) % NT == 0 || A_PART, "A tile/threads");
-    static_assert((BN * CR) % NT == 0 || B_PART, "B tile/threads");
+    constexpr int BUF = conv_lds<BM, BN, RB, EPI>::BUF;
+    static_assert(A_PART || A_CH % NT == 0, "A tile / threads");
+    static_assert(B_CH % NT == 0, "B tile / threads");
     static_assert(TM >= 1 && TN >= 1, "wave tile");
 
-    __shared__ __attribute__((aligned(16))) char smem[2 * (BM + BN) * kRowStride];
-    // buffer b: A tile at smem + b*(BM+BN)*kRowStride, B tile right after it
-    constexpr int kBufBytes = (BM + BN) * kRowStride;
+    __shared__ __attribute__((aligned(16))) char smem[conv_lds<BM, BN, RB, EPI>::BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WN, wn = wid % WN;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
+    const int mt = tile % p.MT, nt = tile / p.MT;
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int IC = p.IC, H = p.H, W = p.W;
     const int K = 9 * IC;
     const int HW = H * W;
-    const int kc = tid % CR;         // this thread's 16-byte chunk within a row
-    const int prow = tid / CR;       // first row this thread loads
+    const int kc = tid % CR;
+    const int prow = tid / CR;
+    const int kpt = IC / BK;                         // k tiles per tap
 
-    // B-loader pixel bookkeeping (fixed across the k loop)
-    int py[B_PER], px[B_PER];
-    int64_t pbase[B_PER];            // element offset of (frame, 0, 0)
-    bool pval[B_PER];
+    const TA *__restrict__ Ap = (const TA *) p.A;
+    const TA *__restrict__ Xp = (const TA *) p.X;
+
+    // loader bookkeeping, fixed over the k loop
+    const TA *aptr[A_PER];
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+        const int row = prow + i * RPP;
+        aptr[i] = Ap + (int64_t) (m0 + (row < BM ? row : 0)) * K + kc * VEC;
+    }
+    const TA *bptr[B_PER];
+    int by[B_PER], bx[B_PER];
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
-        const int n = n0 + prow + i * ROWS_PER_PASS;
-        pval[i] = n < N;
-        const int nn = pval[i] ? n : 0;
-        const int b = nn / HW, rem = nn - b * HW;
-        py[i] = rem / W;
-        px[i] = rem - py[i] * W;
-        pbase[i] = (int64_t) b * x_bstride;
+        const int n = n0 + prow + i * RPP;
+        if (n < p.N) {
+            const int b = n / HW, rem = n - b * HW;
+            by[i] = rem / W;
+            bx[i] = rem - by[i] * W;
+            bptr[i] = Xp + (int64_t) b * p.x_bstride + (int64_t) rem * IC + kc * VEC;
+        } else {
+            by[i] = -(1 << 28);  // every tap out of range: zeros
+            bx[i] = 0;
+            bptr[i] = Xp;
+        }
     }
 
-    uint4 ra[A_PER], rb[B_PER];
-    const int kt_per_tap = IC / BK;
-    const int T = 9 * kt_per_tap;
+    // split-K range of this workgroup
+    const int nsplit = (int) gridDim.y, split = (int) blockIdx.y;
+    const int t_begin = (int) ((int64_t) split * p.T / nsplit);
+    const int t_end = (int) ((int64_t) (split + 1) * p.T / nsplit);
 
-    auto load_tiles = [&](int t) {
-        const int tap = t / kt_per_tap;
-        const int ic0 = (t - tap * kt_per_tap) * BK;
+    u32x4 rr[A_PER + B_PER];  // staged chunks: A in [0, A_PER), B after
+
+    // k tile t -> registers (zero outside the map), registers -> LDS buffer
+    auto load_tile = [&](int t) {
+        const int tap = t / kpt;
+        const int ic0 = (t - tap * kpt) * BK;
         const int dy = tap / 3 - 1, dx = tap % 3 - 1;
-        const int kofs = t * BK + kc * VEC;
-#pragma unroll
-        for (int i = 0; i < A_PER; i++) {
-            if (A_PART && prow >= BM) continue;
-            const int m = m0 + prow + i * ROWS_PER_PASS;
-            ra[i] = *(const uint4 *) (A + (int64_t) m * K + kofs);
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER; i++) {
-            if (B_PART && prow >= BN) continue;
-            const int iy = py[i] + dy, ix = px[i] + dx;
-            if (pval[i] && iy >= 0 && iy < H && ix >= 0 && ix < W) {
-                rb[i] = *(const uint4 *) (X + pbase[i] + (int64_t) (iy * W + ix) * IC + ic0 + kc * VEC);
-            } else {
-                rb[i] = uint4{0u, 0u, 0u, 0u};
-            }
-        }
+        const int aoff = t * BK;
+        const int boff = (dy * W + dx) * IC + ic0;
+        static_for<A_PER>([&](auto i) {
+            if (!A_PART || tid < A_CH) rr[i] = *(const u32x4 *) (aptr[i] + aoff);
+        });
+        static_for<B_PER>([&](auto i) {
+            const int iy = by[i] + dy, ix = bx[i] + dx;
+            if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
+                rr[A_PER + i] = *(const u32x4 *) (bptr[i] + boff);
+            else
+                rr[A_PER + i] = u32x4{0u, 0u, 0u, 0u};
+        });
     };
-    auto store_tiles = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < A_PER; i++)
-            if (!A_PART || prow < BM)
-                *(uint4 *) (smem + buf * kBufBytes + (prow + i * ROWS_PER_PASS) * kRowStride + kc * 16) = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_PER; i++)
-            if (!B_PART || prow < BN)
-                *(uint4 *) (smem + buf * kBufBytes + BM * kRowStride + (prow + i * ROWS_PER_PASS) * kRowStride + kc * 16) = rb[i];
+    auto store_tile = [&](int buf) {
+        char *s_ = smem + buf * BUF;
+        static_for<A_PER>([&](auto i) {
+            if (!A_PART || tid < A_CH) *(u32x4 *) (s_ + (prow + i * RPP) * RS + kc * 16) = rr[i];
+        });
+        static_for<B_PER>([&](auto i) {
+            *(u32x4 *) (s_ + (BM + prow + i * RPP) * RS + kc * 16) = rr[A_PER + i];
+        });
     };
 
     floatx16 acc[TM][TN];
@@ -166,137 +261,278 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
 
-    load_tiles(0);
-    store_tiles(0);
+    if (t_begin < t_end) {
+        load_tile(t_begin);
+        store_tile(0);
+    }
     __syncthreads();
 
     const int lrow = lane & 31;
     const int lk = (lane >> 5) * 16;  // byte offset of this lane's k chunk
-    for (int t = 0; t < T; t++) {
-        const int cur = t & 1;
-        if (t + 1 < T) load_tiles(t + 1);
+    for (int t = t_begin; t < t_end; t++) {
+        const int cur = (t - t_begin) & 1;
+        const bool more = t + 1 < t_end;
+        if (more) load_tile(t + 1);
+        const char *s_ = smem + cur * BUF;
 #pragma unroll
-        for (int ks = 0; ks < kRowBytes / 32; ks++) {
-            uint4 af[TM], bf[TN];
+        for (int ks = 0; ks < RB / 32; ks++) {
+            u32x4 af[TM], bf[TN];
 #pragma unroll
             for (int a = 0; a < TM; a++)
-                af[a] = *(const uint4 *) (smem + cur * kBufBytes + (wm * WTM + a * 32 + lrow) * kRowStride + ks * 32 + lk);
+                af[a] = *(const u32x4 *) (s_ + (wm * WTM + a * 32 + lrow) * RS + ks * 32 + lk);
 #pragma unroll
             for (int b = 0; b < TN; b++)
-                bf[b] = *(const uint4 *) (smem + cur * kBufBytes + BM * kRowStride + (wn * WTN + b * 32 + lrow) * kRowStride + ks * 32 + lk);
+                bf[b] = *(const u32x4 *) (s_ + (BM + wn * WTN + b * 32 + lrow) * RS + ks * 32 + lk);
 #pragma unroll
             for (int a = 0; a < TM; a++)
 #pragma unroll
                 for (int b = 0; b < TN; b++) mfma_op<TA>::run(af[a], bf[b], acc[a][b]);
         }
-        if (t + 1 < T) store_tiles(cur ^ 1);
+        if (more) store_tile(cur ^ 1);
         __syncthreads();
     }
 
-    // epilogue: 1/den, + bias, leaky, * next style, store (4 channels / lane)
+    // accumulator (a, b, v): row = a*32 + (v/4)*8 + (lane/32)*4 + v%4, col = b*32 + lane%32
+    if constexpr (EPI == EPI_STORE || EPI == EPI_PARTIAL) {
 #pragma unroll
-    for (int b = 0; b < TN; b++) {
-        const int n = n0 + wn * WTN + b * 32 + lrow;
-        if (n >= N) continue;
-        const int fr = n / HW, rem = n - fr * HW;
-        const int y = rem / W, x = rem - y * W;
+        for (int b = 0; b < TN; b++) {
+            const int n = n0 + wn * WTN + b * 32 + lrow;
+            if (n >= p.N) continue;
 #pragma unroll
-        for (int a = 0; a < TM; a++) {
+            for (int a = 0; a < TM; a++) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
-                int o;
-                int64_t opix;
-                if (MODE == MODE_DENSE) {
-                    o = m;
-                    opix = n;
-                } else {
-                    const int cls = m / OC;
-                    o = m - cls * OC;
-                    opix = (int64_t) fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
+                for (int i = 0; i < 4; i++) {
+                    const int m = m0 + wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
+                    const float q[4] = {acc[a][b][i * 4], acc[a][b][i * 4 + 1], acc[a][b][i * 4 + 2],
+                                        acc[a][b][i * 4 + 3]};
+                    if constexpr (EPI == EPI_STORE) {
+                        epi_store_quad<TO, MODE>(p, q, m, n);
+                    } else {
+                        float *w = p.ws + ((int64_t) split * p.N + n) * p.M + m;
+                        *(floatx4 *) w = floatx4{q[0], q[1], q[2], q[3]};
+                    }
                 }
-                const floatx4 id = *(const floatx4 *) (inv_den + (int64_t) fr * OC + o);
-                const floatx4 bb = *(const floatx4 *) (bias + o);
-                float v[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
-                if (out_scale) {
-                    const floatx4 sc = *(const floatx4 *) (out_scale + (int64_t) fr * OC + o);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) v[j] *= sc[j];
-                }
-                store4<TO>(Y + opix * OC + o, v[0], v[1], v[2], v[3]);
             }
+        }
+    } else {
+        // EPI_TAIL: BM == OC, one M tile.  Activated tile -> LDS [BN][OC+4] f32
+        constexpr int SOS = BM + 4;
+        float *so = (float *) smem;  // the k loop's buffers are free after its last barrier
+#pragma unroll
+        for (int b = 0; b < TN; b++) {
+            const int col = wn * WTN + b * 32 + lrow;
+            const int n = n0 + col;
+            const int fr = (n < p.N ? n : p.N - 1) / HW;
+#pragma unroll
+            for (int a = 0; a < TM; a++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
+                    const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + row);
+                    const floatx4 bb = *(const floatx4 *) (p.bias + row);
+                    floatx4 v;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                    *(floatx4 *) (so + col * SOS + row) = v;
+                }
+            }
+        }
+        __syncthreads();
+        constexpr int G = BM / 8;            // lanes per pixel
+        constexpr int PPW = 64 / G;          // pixels per wave
+        constexpr int PPB = (NT / 64) * PPW; // pixels per workgroup pass
+        static_assert(BN % PPB == 0, "tail pass");
+        const int gl = lane % G, grp = lane / G;
+        TailWeights tw;
+        load_tail_weights(ta, gl * 8, tw);
+        for (int lp0 = 0; lp0 < BN; lp0 += PPB) {
+            const int lp = lp0 + wid * PPW + grp;
+            const int n = n0 + lp;
+            const bool valid = n < p.N;
+            float ov[8];
+            {
+                const floatx4 x0 = *(const floatx4 *) (so + lp * SOS + gl * 8);
+                const floatx4 x1 = *(const floatx4 *) (so + lp * SOS + gl * 8 + 4);
+                ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
+                ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
+            }
+            tail_pixel<TF, TT, G>(ta, valid ? n : p.N - 1, valid, gl, ov, tw);
         }
     }
 }
 
-// ---------------------------------------------------------------------------
-// launch: pick the tile shape from M (= OC or 4*OC)
+// split-K: sum the partials of every split in order, then the store epilogue
+template <typename TO, int MODE>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ConvParams p, int nsplit) {
+    const int64_t nq = (int64_t) p.N * (p.M / 4);
+    const int64_t NM = (int64_t) p.N * p.M;
+    for (int64_t q = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; q < nq;
+         q += (int64_t) gridDim.x * blockDim.x) {
+        const int n = (int) (q / (p.M / 4));
+        const int m = (int) (q - (int64_t) n * (p.M / 4)) * 4;
+        const float *w = p.ws + (int64_t) n * p.M + m;
+        floatx4 s = *(const floatx4 *) w;
+        for (int k = 1; k < nsplit; k++) {
+            const floatx4 v = *(const floatx4 *) (w + k * NM);
+            s[0] += v[0];
+            s[1] += v[1];
+            s[2] += v[2];
+            s[3] += v[3];
+        }
+        const float acc[4] = {s[0], s[1], s[2], s[3]};
+        epi_store_quad<TO, MODE>(p, acc, m, n);
+    }
+}
 
-template <typename TA, typename TO, int BM, int BN, int WM, int WN, int RB>
-static hipError_t launch_cfg_rb(int mode, const TA *A, const TA *X, TO *Y, const float *inv_den,
-                                const float *bias, const float *out_scale, int N, int H, int W,
-                                int IC, int OC, int64_t x_bstride, hipStream_t st) {
+// ---------------------------------------------------------------------------
+// host side: tile configuration per conv shape
+
+struct TileCfg {
+    int bm, bn, wm, wn;
+};
+
+// fused-tail tiles (BM = OC) and plain tiles by M
+static TileCfg pick_tile(int M, bool fused) {
+    if (fused) {
+        if (M == 128) return {128, 128, 2, 2};
+        if (M == 64) return {64, 256, 1, 4};
+        return {32, 256, 1, 4};
+    }
+    if (M % 128 == 0) return {128, 256, 2, 2};
+    if (M % 64 == 0) return {64, 256, 1, 4};
+    return {32, 256, 1, 4};
+}
+
+static int row_bytes(int IC, int esize) { return (IC * esize) % 128 == 0 ? 128 : 64; }
+
+int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
+
+// split-K factor: a function of the conv's per-frame shape only (never of the
+// number of frames), so a frame's sums do not depend on its batch; sized to
+// give about 256 workgroups at 16 frames
+int modconv_splits(int mode, int H, int W, int IC, int OC, bool f16) {
     const int M = mode == MODE_DENSE ? OC : 4 * OC;
-    dim3 grid((N + BN - 1) / BN, M / BM);
+    const TileCfg tc = pick_tile(M, false);
+    const int esize = f16 ? 2 : 4;
+    const int T = 9 * IC * esize / row_bytes(IC, esize);
+    const int64_t tiles16 = (int64_t) (M / tc.bm) * ((16LL * H * W + tc.bn - 1) / tc.bn);
+    int64_t s = 256 / tiles16;
+    if (s > T / 4) s = T / 4;
+    if (s < 1) s = 1;
+    return (int) s;
+}
+
+int64_t modconv_ws_elems(int mode, int nframes, int H, int W, int IC, int OC, bool f16) {
+    const int s = modconv_splits(mode, H, W, IC, OC, f16);
+    if (s <= 1) return 0;
+    const int M = mode == MODE_DENSE ? OC : 4 * OC;
+    return (int64_t) s * M * nframes * H * W;
+}
+
+template <typename TA, typename TO, int BM, int BN, int WM, int WN, int RB, typename TF, typename TT>
+static hipError_t launch_rb(const ConvParams &p, int mode, int epi, int nsplit, const TailArgs &ta,
+                            hipStream_t st) {
+    const int ntile = p.MT * ((p.N + BN - 1) / BN);
+    dim3 grid((unsigned) ntile, (unsigned) nsplit);
     dim3 block(WM * WN * 64);
-    if (mode == MODE_DENSE)
-        hipLaunchKernelGGL((modconv3x3_kernel<TA, TO, BM, BN, WM, WN, MODE_DENSE, RB>), grid, block,
-                           0, st, A, X, Y, inv_den, bias, out_scale, N, H, W, IC, OC, x_bstride);
-    else
-        hipLaunchKernelGGL((modconv3x3_kernel<TA, TO, BM, BN, WM, WN, MODE_SUBPIX, RB>), grid, block,
-                           0, st, A, X, Y, inv_den, bias, out_scale, N, H, W, IC, OC, x_bstride);
+#define TPMD_K(MODE_, EPI_)                                                                         \
+    hipLaunchKernelGGL((modconv3x3_kernel<TA, TO, BM, BN, WM, WN, RB, MODE_, EPI_, TF, TT>), grid, \
+                       block, 0, st, p, ta)
+    if (epi == EPI_TAIL) {
+        if constexpr (BM <= 128) TPMD_K(MODE_DENSE, EPI_TAIL);
+    } else if (epi == EPI_PARTIAL) {
+        if (mode == MODE_DENSE) TPMD_K(MODE_DENSE, EPI_PARTIAL);
+        else TPMD_K(MODE_SUBPIX, EPI_PARTIAL);
+    } else {
+        if (mode == MODE_DENSE) TPMD_K(MODE_DENSE, EPI_STORE);
+        else TPMD_K(MODE_SUBPIX, EPI_STORE);
+    }
+#undef TPMD_K
     return hipGetLastError();
 }
 
-template <typename TA, typename TO, int BM, int BN, int WM, int WN>
-static hipError_t launch_cfg(int mode, const TA *A, const TA *X, TO *Y, const float *inv_den,
-                             const float *bias, const float *out_scale, int N, int H, int W,
-                             int IC, int OC, int64_t x_bstride, hipStream_t st) {
-    if ((IC * (int) sizeof(TA)) % 128 == 0)
-        return launch_cfg_rb<TA, TO, BM, BN, WM, WN, 128>(mode, A, X, Y, inv_den, bias, out_scale, N,
-                                                          H, W, IC, OC, x_bstride, st);
-    return launch_cfg_rb<TA, TO, BM, BN, WM, WN, 64>(mode, A, X, Y, inv_den, bias, out_scale, N, H,
-                                                     W, IC, OC, x_bstride, st);
+template <typename TA, typename TO, int BM, int BN, int WM, int WN, typename TF, typename TT>
+static hipError_t launch_cfg(const ConvParams &p, int mode, int epi, int nsplit, const TailArgs &ta,
+                             hipStream_t st) {
+    if (row_bytes(p.IC, (int) sizeof(TA)) == 128)
+        return launch_rb<TA, TO, BM, BN, WM, WN, 128, TF, TT>(p, mode, epi, nsplit, ta, st);
+    return launch_rb<TA, TO, BM, BN, WM, WN, 64, TF, TT>(p, mode, epi, nsplit, ta, st);
 }
 
-template <typename TA, typename TO>
-static hipError_t launch_modconv_typed(int mode, const TA *A, const TA *X, TO *Y,
-                                       const float *inv_den, const float *bias,
-                                       const float *out_scale, int nframes, int H, int W, int IC,
-                                       int OC, int64_t x_bstride, hipStream_t st) {
-    const int M = mode == MODE_DENSE ? OC : 4 * OC;
-    const int N = nframes * H * W;
-    if (M % 128 == 0)
-        return launch_cfg<TA, TO, 128, 128, 2, 2>(mode, A, X, Y, inv_den, bias, out_scale, N, H, W,
-                                                  IC, OC, x_bstride, st);
-    if (M % 64 == 0)
-        return launch_cfg<TA, TO, 64, 128, 1, 4>(mode, A, X, Y, inv_den, bias, out_scale, N, H, W,
-                                                 IC, OC, x_bstride, st);
-    return launch_cfg<TA, TO, 32, 256, 1, 4>(mode, A, X, Y, inv_den, bias, out_scale, N, H, W, IC,
-                                             OC, x_bstride, st);
+template <typename TA, typename TO, typename TF, typename TT>
+static hipError_t launch_typed(ConvParams p, int mode, int epi, int nsplit, const TailArgs &ta,
+                               hipStream_t st) {
+    const TileCfg tc = pick_tile(p.M, epi == EPI_TAIL);
+    p.MT = p.M / tc.bm;
+    p.T = 9 * p.IC * (int) sizeof(TA) / row_bytes(p.IC, (int) sizeof(TA));
+    if (tc.bm == 128 && tc.bn == 256)
+        return launch_cfg<TA, TO, 128, 256, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
+    if (tc.bm == 128 && tc.bn == 128)
+        return launch_cfg<TA, TO, 128, 128, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
+    if (tc.bm == 64)
+        return launch_cfg<TA, TO, 64, 256, 1, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
+    return launch_cfg<TA, TO, 32, 256, 1, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
 }
 
-// IC must be a multiple of this (the 64-byte k tile)
-int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
+template <typename TO>
+static hipError_t launch_reduce(const ConvParams &p, int mode, int nsplit, hipStream_t st) {
+    const int64_t nq = (int64_t) p.N * (p.M / 4);
+    int64_t nb = (nq + 255) / 256;
+    if (nb > 65536) nb = 65536;
+    if (mode == MODE_DENSE)
+        hipLaunchKernelGGL((splitk_reduce_kernel<TO, MODE_DENSE>), dim3((unsigned) nb), dim3(256), 0, st,
+                           p, nsplit);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<TO, MODE_SUBPIX>), dim3((unsigned) nb), dim3(256), 0, st,
+                           p, nsplit);
+    return hipGetLastError();
+}
 
-hipError_t launch_modconv(int mode, bool f16, bool out_f16, const void *A, const void *X, void *Y,
-                          const float *inv_den, const float *bias, const float *out_scale,
-                          int nframes, int H, int W, int IC, int OC, int64_t x_bstride,
-                          hipStream_t st) {
-    if (f16) {
-        if (out_f16)
-            return launch_modconv_typed<half_t, half_t>(mode, (const half_t *) A, (const half_t *) X,
-                                                        (half_t *) Y, inv_den, bias, out_scale,
-                                                        nframes, H, W, IC, OC, x_bstride, st);
-        return launch_modconv_typed<half_t, float>(mode, (const half_t *) A, (const half_t *) X,
-                                                   (float *) Y, inv_den, bias, out_scale, nframes,
-                                                   H, W, IC, OC, x_bstride, st);
+hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
+    if (c.nframes <= 0) return hipSuccess;
+    ConvParams p{};
+    p.A = c.A;
+    p.X = c.X;
+    p.Y = c.Y;
+    p.inv_den = c.inv_den;
+    p.bias = c.bias;
+    p.out_scale = c.out_scale;
+    p.ws = c.ws;
+    p.N = c.nframes * c.H * c.W;
+    p.H = c.H;
+    p.W = c.W;
+    p.IC = c.IC;
+    p.OC = c.OC;
+    p.M = c.mode == MODE_DENSE ? c.OC : 4 * c.OC;
+    p.x_bstride = c.x_bstride;
+    const int kal = modconv_k_align(c.f16);
+    if (c.IC % kal != 0 || c.OC % 32 != 0 || (c.mode != MODE_DENSE && c.mode != MODE_SUBPIX))
+        return hipErrorInvalidValue;
+    const bool fused = c.tail != nullptr;
+    if (fused && (c.mode != MODE_DENSE || (c.OC != 32 && c.OC != 64 && c.OC != 128) ||
+                  c.tail->C != c.OC || (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
+        return hipErrorInvalidValue;
+    int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);
+    if (nsplit > 1 && (!c.ws || c.ws_elems < (int64_t) nsplit * p.M * p.N)) nsplit = 1;
+    const int epi = fused ? EPI_TAIL : (nsplit > 1 ? EPI_PARTIAL : EPI_STORE);
+    const TailArgs ta = fused ? *c.tail : TailArgs{};
+    hipError_t e;
+    if (c.f16) {
+        if (fused) {
+            e = c.trunk_f16 ? launch_typed<half_t, float, half_t, half_t>(p, c.mode, epi, 1, ta, st)
+                            : launch_typed<half_t, float, half_t, float>(p, c.mode, epi, 1, ta, st);
+        } else if (c.out_f16) {
+            e = launch_typed<half_t, half_t, half_t, half_t>(p, c.mode, epi, nsplit, ta, st);
+        } else {
+            e = launch_typed<half_t, float, half_t, half_t>(p, c.mode, epi, nsplit, ta, st);
+        }
+    } else {
+        if (c.out_f16 || (fused && c.trunk_f16)) return hipErrorInvalidValue;
+        e = launch_typed<float, float, float, float>(p, c.mode, epi, nsplit, ta, st);
     }
-    return launch_modconv_typed<float, float>(mode, (const float *) A, (const float *) X,
-                                              (float *) Y, inv_den, bias, out_scale, nframes, H, W,
-                                              IC, OC, x_bstride, st);
+    if (e != hipSuccess || epi != EPI_PARTIAL) return e;
+    if (c.f16 && c.out_f16) return launch_reduce<half_t>(p, c.mode, nsplit, st);
+    return launch_reduce<float>(p, c.mode, nsplit, st);
 }
 
 }  // namespace tpmd

@@ -99,10 +99,12 @@ struct tpmd_ctx {
     float *lat = nullptr, *s_all = nullptr, *den_all = nullptr;
     void *xs0 = nullptr, *c1 = nullptr, *trunk = nullptr;
     float *outb = nullptr, *flow[2] = {}, *rgb[2] = {}, *img = nullptr;
+    float *ws = nullptr;              // split-K partials of the low-resolution convs
+    int64_t ws_elems = 0;
 
     // scratch for the per-stage entry points (grow-only)
-    void *scr[3] = {};
-    size_t scr_sz[3] = {};
+    void *scr[4] = {};
+    size_t scr_sz[4] = {};
 
     bool profile = false;
     std::vector<hipEvent_t> ev;
@@ -321,6 +323,10 @@ bool check_ctx(tpmd_ctx *c) {
     }
     return true;
 }
+
+// dense convs whose output channels fit one conv tile run the stage tail in
+// their epilogue (the stage output never goes to HBM)
+bool fused_tail(int oc) { return oc == 32 || oc == 64 || oc == 128; }
 
 // stage entry points run on the caller's stream; NULL is HIP's null stream
 hipStream_t pick_stream(tpmd_ctx *, void *s) { return (hipStream_t) s; }
@@ -584,10 +590,17 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
     for (int j = 0; j < ns; j++) c->st[j].s_off = sg.out0[c->st[j].seg];
 
     size_t act_max = (size_t) 16 * C0, out_max = 0, skip_max = 1;
+    int64_t ws_max = 0;
+    for (int L = 0; L < c->nconv; L++) {
+        const ConvW &cv = c->conv[L];
+        const int j = (L - 1) / 2;
+        const int H = L == 0 ? 4 : (cv.up ? 4 << j : 8 << j);
+        ws_max = std::max(ws_max, modconv_ws_elems(cv.up ? 1 : 0, B, H, H, cv.ic, cv.oc, c->f16));
+    }
     for (int j = 0; j < ns; j++) {
         const size_t r = (size_t) 8 << j;
         act_max = std::max(act_max, r * r * c->oc[j]);
-        out_max = std::max(out_max, r * r * c->oc[j]);
+        if (!fused_tail(c->oc[j])) out_max = std::max(out_max, r * r * c->oc[j]);
         if (j + 1 < ns) skip_max = std::max(skip_max, 3 * r * r);
     }
     const size_t R = (size_t) c->out_res();
@@ -598,7 +611,10 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
     c->xs0 = A((size_t) B * 16 * C0 * c->act_size());
     c->c1 = A((size_t) B * act_max * c->act_size());
     c->trunk = A((size_t) B * act_max * c->act_size());
-    c->outb = (float *) A((size_t) B * out_max * 4);
+    c->outb = (float *) A((size_t) B * std::max<size_t>(out_max, 1) * 4);
+    c->ws_elems = ws_max;
+    c->ws = ws_max > 0 ? (float *) A((size_t) ws_max * 4) : nullptr;
+    if (ws_max > 0 && !c->ws) return -1;
     for (int i = 0; i < 2; i++) {
         c->flow[i] = (float *) A((size_t) B * skip_max * 4);
         c->rgb[i] = (float *) A((size_t) B * skip_max * 4);
@@ -654,6 +670,58 @@ static int set_feats_impl(tpmd_ctx *c, const float *const *feats, bool dev) {
 int tpmd_set_feats(tpmd_ctx *c, const float *const *feats) { return set_feats_impl(c, feats, false); }
 int tpmd_set_feats_device(tpmd_ctx *c, const float *const *feats) { return set_feats_impl(c, feats, true); }
 
+// tail arguments of stage j for frames [0, n) of the decode buffers
+static TailArgs stage_tail_args(tpmd_ctx *c, int j, int n, float *img_dst) {
+    const StageW &s = c->st[j];
+    const bool last = j + 1 == c->ns;
+    TailArgs a{};
+    a.out = c->outb;
+    a.feat = s.feat;
+    a.wflow = s.wflow;
+    a.sflow = c->s_all + s.s_off;
+    a.fbias = s.fbias;
+    a.fup = s.fup;
+    a.flow_prev = j > 0 ? c->flow[(j - 1) & 1] : nullptr;
+    a.flow_cur = last ? nullptr : c->flow[j & 1];
+    a.lin = s.lin;
+    a.wrgb = s.wrgb;
+    a.rlb = s.rlb;
+    a.rbias = s.rbias;
+    a.rup = s.rup;
+    a.rgb_prev = j > 0 ? c->rgb[(j - 1) & 1] : nullptr;
+    a.rgb_cur = last ? img_dst : c->rgb[j & 1];
+    a.s_next = last ? nullptr : c->s_all + c->conv[3 + 2 * j].s_off;
+    a.trunk = last ? nullptr : c->trunk;
+    a.warp_tap = nullptr;
+    a.nframes = n;
+    a.r = 8 << j;
+    a.C = c->oc[j];
+    return a;
+}
+
+static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void *X, void *Y,
+                          const float *out_scale, bool out_f16) {
+    ConvArgs a;
+    a.mode = cv.up ? 1 : 0;
+    a.f16 = c->f16;
+    a.out_f16 = out_f16;
+    a.A = cv.A;
+    a.X = X;
+    a.Y = Y;
+    a.inv_den = c->den_all + cv.d_off;
+    a.bias = cv.bias;
+    a.out_scale = out_scale;
+    a.nframes = n;
+    a.H = H;
+    a.W = H;
+    a.IC = cv.ic;
+    a.OC = cv.oc;
+    a.x_bstride = (int64_t) H * H * cv.ic;
+    a.ws = c->ws;
+    a.ws_elems = c->ws_elems;
+    return a;
+}
+
 static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
     hipStream_t st = c->stream;
     const bool f16 = c->f16;
@@ -669,49 +737,30 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
     if (!c->hip_ok(launch_prescale_input(f16, c->input_cl, c->s_all + k1.s_off, c->xs0, C0, n, st), "prescale"))
         return false;
     // conv1 -> trunk (pre-scaled by the stage-0 up-conv style)
-    if (!c->hip_ok(launch_modconv(0, f16, f16, k1.A, c->xs0, c->trunk, c->den_all + k1.d_off, k1.bias,
-                                  c->s_all + c->conv[1].s_off, n, 4, 4, C0, C0, (int64_t) 16 * C0, st),
+    if (!c->hip_ok(launch_modconv(conv_args(c, k1, n, 4, c->xs0, c->trunk, c->s_all + c->conv[1].s_off, f16), st),
                    "conv1"))
         return false;
     for (int j = 0; j < ns; j++) {
-        const int r = 8 << j, rh = r / 2, C = c->oc[j], IC = c->ic[j];
-        const bool last = j + 1 == ns;
+        const int r = 8 << j, rh = r / 2, C = c->oc[j];
         const ConvW &up = c->conv[1 + 2 * j], &dn = c->conv[2 + 2 * j];
         mark();
-        if (!c->hip_ok(launch_modconv(1, f16, f16, up.A, c->trunk, c->c1, c->den_all + up.d_off, up.bias,
-                                      c->s_all + dn.s_off, n, rh, rh, IC, C, (int64_t) rh * rh * IC, st),
+        if (!c->hip_ok(launch_modconv(conv_args(c, up, n, rh, c->trunk, c->c1, c->s_all + dn.s_off, f16), st),
                        "up-conv"))
             return false;
         mark();
-        if (!c->hip_ok(launch_modconv(0, f16, false, dn.A, c->c1, c->outb, c->den_all + dn.d_off, dn.bias,
-                                      nullptr, n, r, r, C, C, (int64_t) r * r * C, st),
-                       "conv"))
-            return false;
-        mark();
-        const StageW &s = c->st[j];
-        TailArgs a{};
-        a.out = c->outb;
-        a.feat = s.feat;
-        a.wflow = s.wflow;
-        a.sflow = c->s_all + s.s_off;
-        a.fbias = s.fbias;
-        a.fup = s.fup;
-        a.flow_prev = j > 0 ? c->flow[(j - 1) & 1] : nullptr;
-        a.flow_cur = last ? nullptr : c->flow[j & 1];
-        a.lin = s.lin;
-        a.wrgb = s.wrgb;
-        a.rlb = s.rlb;
-        a.rbias = s.rbias;
-        a.rup = s.rup;
-        a.rgb_prev = j > 0 ? c->rgb[(j - 1) & 1] : nullptr;
-        a.rgb_cur = last ? img_dst : c->rgb[j & 1];
-        a.s_next = last ? nullptr : c->s_all + c->conv[3 + 2 * j].s_off;
-        a.trunk = last ? nullptr : c->trunk;
-        a.warp_tap = nullptr;
-        a.nframes = n;
-        a.r = r;
-        a.C = C;
-        if (!c->hip_ok(launch_stage_tail(a, f16, false, f16, st), "tail")) return false;
+        const TailArgs ta = stage_tail_args(c, j, n, img_dst);
+        if (fused_tail(C)) {
+            ConvArgs ca = conv_args(c, dn, n, r, c->c1, nullptr, nullptr, false);
+            ca.tail = &ta;
+            ca.trunk_f16 = f16;
+            if (!c->hip_ok(launch_modconv(ca, st), "conv+tail")) return false;
+            mark();
+        } else {
+            if (!c->hip_ok(launch_modconv(conv_args(c, dn, n, r, c->c1, c->outb, nullptr, false), st), "conv"))
+                return false;
+            mark();
+            if (!c->hip_ok(launch_stage_tail(ta, f16, false, f16, st), "tail")) return false;
+        }
     }
     mark();
     return true;
@@ -820,10 +869,26 @@ int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, con
     t.d0[0] = 0;
     if (!c->hip_ok(launch_demod(c->saug_all, s, den, t, n, st), "demod")) return -1;
     if (!c->hip_ok(launch_prescale_map(c->f16, x, s, xs, cv.ic, npix, n, st), "prescale")) return -1;
-    if (!c->hip_ok(launch_modconv(cv.up ? 1 : 0, c->f16, false, cv.A, xs, y, den, cv.bias, nullptr, n, H, W,
-                                  cv.ic, cv.oc, npix * cv.ic, st),
-                   "modconv"))
-        return -1;
+    ConvArgs ca;
+    ca.mode = cv.up ? 1 : 0;
+    ca.f16 = c->f16;
+    ca.A = cv.A;
+    ca.X = xs;
+    ca.Y = y;
+    ca.inv_den = den;
+    ca.bias = cv.bias;
+    ca.nframes = n;
+    ca.H = H;
+    ca.W = W;
+    ca.IC = cv.ic;
+    ca.OC = cv.oc;
+    ca.x_bstride = npix * cv.ic;
+    ca.ws_elems = modconv_ws_elems(ca.mode, n, H, W, cv.ic, cv.oc, c->f16);
+    if (ca.ws_elems > 0) {
+        ca.ws = (float *) c->scratch(3, (size_t) ca.ws_elems * 4);
+        if (!ca.ws) return -1;
+    }
+    if (!c->hip_ok(launch_modconv(ca, st), "modconv")) return -1;
     return 0;
 }
 
@@ -867,6 +932,88 @@ int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_
     a.r = 8 << j;
     a.C = c->oc[j];
     return c->hip_ok(launch_stage_tail(a, c->f16, false, false, pick_stream(c, stream)), "tail") ? 0 : -1;
+}
+
+int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float *s_conv, const float *s_flow,
+                         const float *flow_prev, const float *rgb_prev, float *flow, float *trunk, float *rgb,
+                         float *warp, void *stream) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built || !c->feats_set) {
+        c->err = "decoder not built / feats not set";
+        return -1;
+    }
+    if (j < 0 || j >= c->ns || !c1 || !s_conv || !s_flow || !rgb || n < 1) {
+        c->err = "tpmd_stage_conv_tail: bad arguments";
+        return -1;
+    }
+    if (j > 0 && (!flow_prev || !rgb_prev)) {
+        c->err = "tpmd_stage_conv_tail: stages > 0 need flow_prev and rgb_prev";
+        return -1;
+    }
+    hipStream_t st = pick_stream(c, stream);
+    const ConvW &cv = c->conv[2 + 2 * j];
+    const int r = 8 << j, C = c->oc[j];
+    const int64_t npix = (int64_t) r * r;
+    void *xs = c->scratch(1, (size_t) n * npix * C * c->act_size());
+    float *den = (float *) c->scratch(2, (size_t) n * C * 4);
+    if (!xs || !den) return -1;
+    DemodTable t{};
+    t.n = 1;
+    t.row0[0] = 0;
+    t.row0[1] = cv.oc;
+    t.ic[0] = cv.ic;
+    t.oc[0] = cv.oc;
+    t.saug0[0] = cv.saug_off;
+    if (!c->hip_ok(launch_demod(c->saug_all, s_conv, den, t, n, st), "demod")) return -1;
+    if (!c->hip_ok(launch_prescale_map(c->f16, c1, s_conv, xs, C, npix, n, st), "prescale")) return -1;
+    TailArgs a{};
+    a.feat = c->st[j].feat;
+    a.wflow = c->st[j].wflow;
+    a.sflow = s_flow;
+    a.fbias = c->st[j].fbias;
+    a.fup = c->st[j].fup;
+    a.flow_prev = j > 0 ? flow_prev : nullptr;
+    a.flow_cur = flow;
+    a.lin = c->st[j].lin;
+    a.wrgb = c->st[j].wrgb;
+    a.rlb = c->st[j].rlb;
+    a.rbias = c->st[j].rbias;
+    a.rup = c->st[j].rup;
+    a.rgb_prev = j > 0 ? rgb_prev : nullptr;
+    a.rgb_cur = rgb;
+    a.trunk = trunk;
+    a.warp_tap = warp;
+    a.nframes = n;
+    a.r = r;
+    a.C = C;
+    ConvArgs ca;
+    ca.mode = 0;
+    ca.f16 = c->f16;
+    ca.A = cv.A;
+    ca.X = xs;
+    ca.inv_den = den;
+    ca.bias = cv.bias;
+    ca.nframes = n;
+    ca.H = r;
+    ca.W = r;
+    ca.IC = C;
+    ca.OC = C;
+    ca.x_bstride = npix * C;
+    ca.ws_elems = modconv_ws_elems(0, n, r, r, C, C, c->f16);
+    if (ca.ws_elems > 0) {
+        ca.ws = (float *) c->scratch(3, (size_t) ca.ws_elems * 4);
+        if (!ca.ws) return -1;
+    }
+    if (fused_tail(C)) {
+        ca.tail = &a;
+        return c->hip_ok(launch_modconv(ca, st), "conv+tail") ? 0 : -1;
+    }
+    float *out = (float *) c->scratch(0, (size_t) n * npix * C * 4);
+    if (!out) return -1;
+    ca.Y = out;
+    if (!c->hip_ok(launch_modconv(ca, st), "conv")) return -1;
+    a.out = out;
+    return c->hip_ok(launch_stage_tail(a, c->f16, false, false, st), "tail") ? 0 : -1;
 }
 
 // ---- op-level

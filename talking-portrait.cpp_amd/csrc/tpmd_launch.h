@@ -57,11 +57,33 @@ hipError_t launch_upfirdn2x(const float *x, const float *k4, float *y, int W, in
 hipError_t launch_flow_grid(const float *fl, const float *xs, float *y, int64_t N,
                             hipStream_t st);
 
+// one modulated 3x3 conv launch (k_conv.hip)
+struct ConvArgs {
+    int mode = 0;               // 0 dense, 1 composed sub-pixel up-conv
+    bool f16 = false;           // operands f16 (else f32)
+    bool out_f16 = false;       // stored activation f16 (f16 mode only)
+    const void *A = nullptr;    // [M][9*IC], M = OC or 4*OC
+    const void *X = nullptr;    // CL input [frame][H][W][IC], frame stride x_bstride
+    void *Y = nullptr;          // CL output [frame][H'][W'][OC]
+    const float *inv_den = nullptr;    // [frame][OC]
+    const float *bias = nullptr;       // [OC]
+    const float *out_scale = nullptr;  // [frame][OC] or null
+    int nframes = 0, H = 0, W = 0, IC = 0, OC = 0;
+    int64_t x_bstride = 0;
+    float *ws = nullptr;        // split-K workspace, ws_elems floats
+    int64_t ws_elems = 0;
+    // fused stage tail (dense conv with OC in {32, 64, 128}): the conv output
+    // stays on chip; Y is unused and the tail's outputs are written instead
+    const TailArgs *tail = nullptr;
+    bool trunk_f16 = false;
+};
+
 int modconv_k_align(bool f16);
-hipError_t launch_modconv(int mode, bool f16, bool out_f16, const void *A, const void *X, void *Y,
-                          const float *inv_den, const float *bias, const float *out_scale,
-                          int nframes, int H, int W, int IC, int OC, int64_t x_bstride,
-                          hipStream_t st);
+// split-K factor of a conv (depends on the per-frame shape only)
+int modconv_splits(int mode, int H, int W, int IC, int OC, bool f16);
+// workspace floats a conv needs for nframes frames (0 = no split)
+int64_t modconv_ws_elems(int mode, int nframes, int H, int W, int IC, int OC, bool f16);
+hipError_t launch_modconv(const ConvArgs &c, hipStream_t st);
 
 hipError_t launch_stage_tail(const TailArgs &a, bool feat_f16, bool out_f16, bool trunk_f16,
                              hipStream_t st);

@@ -66,6 +66,7 @@ def lib():
             "tpmd_stage_times": (I, [P, P, I]),
             "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
             "tpmd_stage_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P]),
+            "tpmd_stage_conv_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P, P]),
             "tpmd_gather": (I, [P, I, I, I, I, P, I64, I, I, P, P]),
             "tpmd_gather_taps": (I, [P, I, I, I64, I, P, P, P, P, P]),
             "tpmd_upfirdn2x": (I, [P, P, P, I, I, I64, P]),
@@ -235,6 +236,13 @@ class MotionDecoder:
         self._check(lib().tpmd_stage_tail(self.h, j, _ptr(out), n, _ptr(s_flow), _ptr(flow_prev),
                                           _ptr(rgb_prev), _ptr(flow), _ptr(trunk), _ptr(rgb),
                                           _ptr(warp), _stream(stream)))
+
+    def stage_conv_tail(self, j, c1, s_conv, s_flow, flow_prev, rgb_prev, flow, trunk, rgb, warp,
+                        stream=None):
+        n = c1.shape[0]
+        self._check(lib().tpmd_stage_conv_tail(self.h, j, _ptr(c1), n, _ptr(s_conv), _ptr(s_flow),
+                                               _ptr(flow_prev), _ptr(rgb_prev), _ptr(flow), _ptr(trunk),
+                                               _ptr(rgb), _ptr(warp), _stream(stream)))
 
 
 # ---- op level (torch cuda tensors)

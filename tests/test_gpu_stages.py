@@ -123,3 +123,41 @@ def test_tail_all_stages_small(om, torch_cuda, ftype):
             e = rel_l2(t[k].cpu().numpy(), w)
             assert e <= 1e-4, (j, k, e)
         skf, sk = fl, rgb
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+@pytest.mark.parametrize("ic,oc", [
+    (SMALL_IC, SMALL_OC),                                  # fused stages (C <= 128)
+    ((512, 512, 512, 512, 256, 128, 64), (512, 512, 512, 256, 128, 64, 32)),  # reference widths
+])
+def test_conv_tail_all_stages(om, torch_cuda, ftype, ic, oc):
+    """dense conv + stage tail as decode runs them (one fused kernel when
+    C <= 128), against the oracle's styled_conv followed by its tail.  The
+    conv output differs from the oracle's at rounding level, and the warp
+    amplifies flow differences by ~r/2, so this runs on the well-conditioned
+    workload (the tail alone is checked on i.i.d. inputs above)"""
+    torch = torch_cuda
+    ref, dec, lat = _pair(om, ftype, ic, oc, workload="smooth")
+    g = np.random.default_rng(14)
+    nf = lat.shape[0]
+    for j in range(len(oc)):
+        r, C = 8 << j, oc[j]
+        if r * r * C * nf > (1 << 23) and j < len(oc) - 1:
+            continue                                      # keep the oracle side quick
+        base = f"dec.convs.{2 * j + 1}"
+        c1 = g.standard_normal((nf, r * r, C)).astype(np.float32)
+        s = ref.style_of(base + ".conv", lat)
+        out = ref._styled_conv_cl(c1, r, r, base, s, ref.demod_den(base + ".conv.weight", s))
+        fs = ref.style_of(f"dec.to_flows.{j}.conv", lat)
+        skf = sk = None
+        if j > 0:
+            skf = g.standard_normal((nf, 3, r // 2, r // 2)).astype(np.float32) * 0.3
+            sk = g.standard_normal((nf, 3, r // 2, r // 2)).astype(np.float32)
+        fl, warp, trunk, rgb = ref.tail_cl(j, out, fs, skf, sk)
+        t = {"flow": torch.empty((nf, 3, r, r), device="cuda"), "trunk": torch.empty((nf, r * r, C), device="cuda"),
+             "rgb": torch.empty((nf, 3, r, r), device="cuda"), "warp": torch.empty((nf, r * r, C), device="cuda")}
+        dec.stage_conv_tail(j, _dev(torch, c1), _dev(torch, s), _dev(torch, fs),
+                            None if skf is None else _dev(torch, skf), None if sk is None else _dev(torch, sk),
+                            t["flow"], t["trunk"], t["rgb"], t["warp"])
+        for k, w in (("flow", fl), ("warp", warp), ("trunk", trunk), ("rgb", rgb)):
+            _check(ftype, t[k].cpu().numpy(), w, (j, k))
