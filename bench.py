@@ -24,9 +24,11 @@ PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}
 REF_FPS_RTX5070TI = 213.2   # mdec, GGML-CUDA f16 fast graph (docs/vulkan-perf.md:134,143)
 
 
-def fused_tail(oc):
-    """stages whose dense conv runs the stage tail in its epilogue"""
-    return oc in (32, 64, 128)
+def fused_tail(oc, r):
+    """stages whose dense conv runs the stage tail in its epilogue: all
+    channels in one conv tile, the tile's pixels in one frame"""
+    bn = 256 if oc == 32 else 128
+    return oc in (32, 64, 128) and (r * r) % bn == 0
 
 
 def stage_costs(ic, oc, nframes, ftype):
@@ -53,7 +55,7 @@ def stage_costs(ic, oc, nframes, ftype):
         b_tl = (r * r * OC * sa + (nframes * 2 * 3 * (r // 2) ** 2 * 4 if j else 0)
                 + (0 if last else px * OC * sa + px * 3 * 4) + px * 3 * 4)
         f_tl = px * OC * 2 * 6
-        if fused_tail(OC):
+        if fused_tail(OC, r):
             b_dt = px * OC * sa + 9 * OC * OC * sw + b_tl
             slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv+tail", f_dn + f_tl, b_dt), None]
         else:

@@ -152,7 +152,7 @@ struct conv_lds {
     static constexpr int RS = RB + 16;                  // padded row stride (bytes)
     static constexpr int BUF = (BM + BN) * RS;
     static constexpr int KLOOP = 2 * BUF;
-    static constexpr int TAIL = EPI == EPI_TAIL ? BN * (BM + 4) * 4 : 0;
+    static constexpr int TAIL = EPI == EPI_TAIL ? tile_tail_lds<BM, BN>::FLOATS * 4 : 0;
     static constexpr int BYTES = KLOOP > TAIL ? KLOOP : TAIL;
 };
 
@@ -315,14 +315,15 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, T
             }
         }
     } else {
-        // EPI_TAIL: BM == OC, one M tile.  Activated tile -> LDS [BN][OC+4] f32
-        constexpr int SOS = BM + 4;
-        float *so = (float *) smem;  // the k loop's buffers are free after its last barrier
+        // EPI_TAIL: BM == OC, one M tile, BN pixels of one frame.  The
+        // activated tile goes to LDS [BN][OC+4] f32, then the stage tail runs
+        // on it (the k loop's buffers are free after its last barrier)
+        constexpr int SOS = tile_tail_lds<BM, BN>::SOS;
+        float *so = (float *) smem;
+        const int fr = n0 / HW;
 #pragma unroll
         for (int b = 0; b < TN; b++) {
             const int col = wn * WTN + b * 32 + lrow;
-            const int n = n0 + col;
-            const int fr = (n < p.N ? n : p.N - 1) / HW;
 #pragma unroll
             for (int a = 0; a < TM; a++) {
 #pragma unroll
@@ -337,27 +338,7 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, T
                 }
             }
         }
-        __syncthreads();
-        constexpr int G = BM / 8;            // lanes per pixel
-        constexpr int PPW = 64 / G;          // pixels per wave
-        constexpr int PPB = (NT / 64) * PPW; // pixels per workgroup pass
-        static_assert(BN % PPB == 0, "tail pass");
-        const int gl = lane % G, grp = lane / G;
-        TailWeights tw;
-        load_tail_weights(ta, gl * 8, tw);
-        for (int lp0 = 0; lp0 < BN; lp0 += PPB) {
-            const int lp = lp0 + wid * PPW + grp;
-            const int n = n0 + lp;
-            const bool valid = n < p.N;
-            float ov[8];
-            {
-                const floatx4 x0 = *(const floatx4 *) (so + lp * SOS + gl * 8);
-                const floatx4 x1 = *(const floatx4 *) (so + lp * SOS + gl * 8 + 4);
-                ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
-                ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
-            }
-            tail_pixel<TF, TT, G>(ta, valid ? n : p.N - 1, valid, gl, ov, tw);
-        }
+        tile_tail<TF, TT, BM, BN, NT>(ta, so, n0, p.N, tid);
     }
 }
 
@@ -395,7 +376,7 @@ struct TileCfg {
 static TileCfg pick_tile(int M, bool fused) {
     if (fused) {
         if (M == 128) return {128, 128, 2, 2};
-        if (M == 64) return {64, 256, 1, 4};
+        if (M == 64) return {64, 128, 1, 4};
         return {32, 256, 1, 4};
     }
     if (M % 128 == 0) return {128, 256, 2, 2};
@@ -406,6 +387,14 @@ static TileCfg pick_tile(int M, bool fused) {
 static int row_bytes(int IC, int esize) { return (IC * esize) % 128 == 0 ? 128 : 64; }
 
 int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
+
+// the dense conv of an r x r stage with OC channels can run the stage tail in
+// its epilogue: one tile holds every channel and its pixels lie in one frame
+bool modconv_fusable(int OC, int r) {
+    if (OC != 32 && OC != 64 && OC != 128) return false;
+    const TileCfg tc = pick_tile(OC, true);
+    return (r * r) % tc.bn == 0;
+}
 
 // split-K factor: a function of the conv's per-frame shape only (never of the
 // number of frames), so a frame's sums do not depend on its batch; sized to
@@ -469,6 +458,8 @@ static hipError_t launch_typed(ConvParams p, int mode, int epi, int nsplit, cons
         return launch_cfg<TA, TO, 128, 256, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
     if (tc.bm == 128 && tc.bn == 128)
         return launch_cfg<TA, TO, 128, 128, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
+    if (tc.bm == 64 && tc.bn == 128)
+        return launch_cfg<TA, TO, 64, 128, 1, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
     if (tc.bm == 64)
         return launch_cfg<TA, TO, 64, 256, 1, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
     return launch_cfg<TA, TO, 32, 256, 1, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
@@ -509,8 +500,9 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (c.IC % kal != 0 || c.OC % 32 != 0 || (c.mode != MODE_DENSE && c.mode != MODE_SUBPIX))
         return hipErrorInvalidValue;
     const bool fused = c.tail != nullptr;
-    if (fused && (c.mode != MODE_DENSE || (c.OC != 32 && c.OC != 64 && c.OC != 128) ||
-                  c.tail->C != c.OC || (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
+    if (fused && !modconv_fusable(c.OC, c.H) ) return hipErrorInvalidValue;
+    if (fused && (c.mode != MODE_DENSE || c.H != c.W || c.tail->C != c.OC || c.tail->r != c.H ||
+                  (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
         return hipErrorInvalidValue;
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);
     if (nsplit > 1 && (!c.ws || c.ws_elems < (int64_t) nsplit * p.M * p.N)) nsplit = 1;

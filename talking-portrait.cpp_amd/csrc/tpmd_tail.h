@@ -169,3 +169,168 @@ __device__ __forceinline__ void tail_pixel(const TailArgs &a, int64_t pp, bool v
 }
 
 }  // namespace tpmd
+
+namespace tpmd {
+
+// ---------------------------------------------------------------------------
+// Stage tail of a tile of BN consecutive pixels of ONE frame whose dense-conv
+// output (after bias + leaky) sits in LDS, run by the NT threads of a
+// workgroup in two phases (same arithmetic as tail_pixel):
+//   phase 1, one thread per pixel: ToFlow dot (the style-folded weights
+//     Wf * s_f of the tile's frame are staged in LDS), flow skip, flow head,
+//     bilinear tap geometry, rgb skip; the per-pixel results go to LDS;
+//   phase 2, G = C/8 lanes per pixel: gather of the feature taps, warp,
+//     trunk (* next style, stored), ToRGB with a butterfly over the G lanes.
+// Per-pixel scalar work runs once instead of on each of the G lanes.
+template <int C, int BN>
+struct tile_tail_lds {
+    static constexpr int SOS = C + 4;                 // out row stride (floats)
+    static constexpr int PRM = 8;                     // per-pixel record (floats)
+    static constexpr int OUT = BN * SOS;              // offsets in floats
+    static constexpr int PRM0 = OUT;
+    static constexpr int WFS0 = PRM0 + BN * PRM;
+    static constexpr int FLOATS = WFS0 + 3 * C;
+};
+
+template <typename TF, typename TT, int C, int BN, int NT>
+__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int N, int tid) {
+#pragma clang fp contract(off)
+    typedef tile_tail_lds<C, BN> L;
+    constexpr int G = C / 8;
+    constexpr int PPW = 64 / G;
+    constexpr int PPB = (NT / 64) * PPW;
+    static_assert(BN % PPB == 0, "tail pass");
+    const int r = a.r, rh = r >> 1;
+    const int RR = r * r;
+    const int fr = n0 / RR;                          // the tile lies in one frame
+    float *so = lds, *prm = lds + L::PRM0, *wfs = lds + L::WFS0;
+
+    // folded ToFlow weights of this frame (gemm_weight: W * s rounded to f32)
+    for (int i = tid; i < 3 * C; i += NT) {
+        const int c = i % C;
+        wfs[i] = a.wflow[i] * a.sflow[(int64_t) fr * C + c];
+    }
+    __syncthreads();
+
+    // ---- phase 1: one thread per pixel
+    if (tid < BN) {
+        const int p = tid;
+        const int n = n0 + p < N ? n0 + p : N - 1;
+        const int pix = n - fr * RR;
+        const int y = pix / r, x = pix - y * r;
+        float fl[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < C; c += 4) {
+            const floatx4 o = *(const floatx4 *) (so + p * L::SOS + c);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                fl[k] = __builtin_fmaf(wfs[k * C + c], o[0], fl[k]);
+                fl[k] = __builtin_fmaf(wfs[k * C + c + 1], o[1], fl[k]);
+                fl[k] = __builtin_fmaf(wfs[k * C + c + 2], o[2], fl[k]);
+                fl[k] = __builtin_fmaf(wfs[k * C + c + 3], o[3], fl[k]);
+            }
+        }
+        float up[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            fl[k] = fl[k] + a.fbias[k];
+            if (a.flow_prev)
+                fl[k] = fl[k] + upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
+            if (a.rgb_prev) up[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+        }
+        if (a.flow_cur && n0 + p < N) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) a.flow_cur[((int64_t) fr * 3 + k) * RR + pix] = fl[k];
+        }
+        const float gx = tanhf(fl[0]) + a.lin[x];
+        const float gy = tanhf(fl[1]) + a.lin[y];
+        const float m = 1.0f / (1.0f + expf(-fl[2]));
+        const taps4 t = gather_geometry(gx, gy, r, r);
+        *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
+        *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, up[0], up[1], up[2]};
+    }
+    __syncthreads();
+
+    // ---- phase 2: G lanes per pixel, 8 channels each
+    const int lane = tid & 63, wid = tid >> 6;
+    const int gl = lane % G, grp = lane / G;
+    const int c0 = gl * 8;
+    float wr[3][8], sn[8];
+#pragma unroll
+    for (int k = 0; k < 3; k++) load8<float>::run(a.wrgb + k * C + c0, wr[k]);
+    if (a.s_next) load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
+    const TF *feat = (const TF *) a.feat;
+    for (int lp0 = 0; lp0 < BN; lp0 += PPB) {
+        const int lp = lp0 + wid * PPW + grp;
+        const int n = n0 + lp;
+        const bool valid = n < N;
+        const floatx4 q0 = *(const floatx4 *) (prm + lp * L::PRM);
+        const floatx4 q1 = *(const floatx4 *) (prm + lp * L::PRM + 4);
+        taps4 t;
+        t.x0 = __float_as_int(q0[0]);
+        t.y0 = __float_as_int(q0[1]);
+        t.wx = q0[2];
+        t.wy = q0[3];
+        const float m = q1[0];
+        float fv[4][8];
+        bool in[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
+            in[k] = cx >= 0 && cx < r && cy >= 0 && cy < r;
+            if (in[k]) load8<TF>::run(feat + (int64_t) (cy * r + cx) * C + c0, fv[k]);
+        }
+        float ov[8];
+        {
+            const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
+            const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
+            ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
+            ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
+        }
+        float smp[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) smp[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (!in[k]) continue;
+            const float wk = tap_weight(t, k);
+#pragma unroll
+            for (int e = 0; e < 8; e++) smp[e] += wk * fv[k][e];
+        }
+        float warp[8], trunk[8];
+        const float one_m = 1.0f - m;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            warp[e] = smp[e] * m;
+            trunk[e] = warp[e] + ov[e] * one_m;
+        }
+        const int64_t pp = valid ? n : N - 1;
+        if (valid && a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
+        if (valid && a.trunk) {
+            if (a.s_next) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
+            }
+            store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
+        }
+        float rgb[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc = __builtin_fmaf(wr[k][e], warp[e], acc);
+            rgb[k] = group_sum<G>(acc);
+        }
+        if (valid && gl < 3) {
+            const int k = gl;
+            const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
+            float v = leaky(rv + a.rlb[k]);
+            v = v + a.rbias[k];
+            if (a.rgb_prev) v = v + (k == 0 ? q1[1] : (k == 1 ? q1[2] : q1[3]));
+            const int pix = n - fr * RR;
+            a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
+        }
+    }
+}
+
+}  // namespace tpmd
