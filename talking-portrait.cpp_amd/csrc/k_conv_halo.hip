@@ -1,0 +1,252 @@
+// Modulated 3x3 convolution for the high-resolution, few-channel stages
+// (input channels IC in {32, 64}, GEMM rows M in {32, 64, 128}; f16 operands):
+// the same implicit GEMM as k_conv.hip, Y[m][n] = sum_k A[m][k] X(k, n) with
+// k = tap*IC + ic, organised so that neither operand is re-read per tap:
+//
+//   * A stationary in registers.  Each wave owns 32 GEMM rows and keeps
+//     their 9*IC columns as MFMA A fragments for the whole kernel (72 VGPRs
+//     for IC = 32, 144 for IC = 64).
+//   * B as a halo tile in LDS.  A workgroup computes a TH x 32 block of
+//     output pixels of one frame; the (TH+2) x 34 input pixels around it (all
+//     IC channels, zero outside the map) are staged in LDS once, and each tap
+//     reads its B fragments as a shifted window of that tile — the im2col of
+//     the reference (src/motion_dec.cpp:340-354) is never formed, and every
+//     input byte leaves L2 about (TH+2)*34 / (TH*32) times instead of 9.
+//   * Persistent workgroups.  Each workgroup walks tiles t, t + grid, ...;
+//     the next tile's halo is loaded into registers while the current one is
+//     multiplied, so a tile costs one LDS commit and two barriers.
+//
+// Epilogues as k_conv.hip: EPI_STORE (dense or composed sub-pixel up-conv
+// store, 1/den + bias + leaky + next style) or EPI_TAIL (dense conv whose
+// activated tile goes to LDS for the two-phase stage tail, tpmd_tail.h).
+//
+// MFMA: v_mfma_f32_32x32x16_f16; a 32-column block of the output is one row
+// of the tile (32 consecutive pixels), lane % 32 its column.
+#include "tpmd_conv.h"
+
+namespace tpmd {
+
+template <int IC, int M, int EPI>
+struct halo_cfg {
+    static constexpr int NT = 256;
+    static constexpr int WM = M / 32, WN = 4 / WM;       // waves along M / along tile rows
+    static constexpr int TH = (M == 128 || (IC == 64 && EPI == EPI_TAIL)) ? 4 : 8;
+    static constexpr int TW = 32;
+    static constexpr int TN = TH / WN;                  // tile rows per wave
+    static constexpr int BN = TH * TW;                  // pixels per tile
+    static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
+    static constexpr int ROWB = IC * 2 + 16;            // padded halo pixel (bytes)
+    static constexpr int CPP = IC * 2 / 16;             // 16-byte chunks per pixel
+    static constexpr int HCH = HPX * CPP;
+    static constexpr int PF = (HCH + NT - 1) / NT;      // prefetch chunks per thread
+    static constexpr int KS = IC / 16;                  // MFMA k steps per tap
+    static constexpr int NAF = 9 * KS;                  // A fragments per wave
+    static constexpr int HALO_BYTES = HPX * ROWB;
+    static constexpr int TAIL_BYTES = EPI == EPI_TAIL ? tile_tail_lds<M, BN>::FLOATS * 4 : 0;
+    static constexpr int LDS = HALO_BYTES > TAIL_BYTES ? HALO_BYTES : TAIL_BYTES;
+    static_assert(WM * WN == 4 && TN * WN == TH, "wave layout");
+};
+
+template <int IC, int M, int MODE, int EPI, typename TO, typename TT>
+__global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArgs ta, int tiles_x,
+                                                           int tiles_y, int ntiles) {
+    typedef halo_cfg<IC, M, EPI> C;
+    typedef half_t TA;
+    constexpr int NT = C::NT, TW = C::TW, TN = C::TN, HWD = C::HWD, ROWB = C::ROWB;
+    constexpr int CPP = C::CPP, HCH = C::HCH, PF = C::PF, KS = C::KS, NAF = C::NAF;
+    __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / C::WN, wn = wid % C::WN;
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * 16;
+    const int H = p.H, W = p.W;
+    const int K = 9 * IC;
+
+    // this wave's A rows wm*32 + lane%32, all 9*IC columns: fragment f holds
+    // k = f*16 + (lane/32)*8 .. +8 (f = tap*KS + ks)
+    u32x4 af[NAF];
+    {
+        const TA *arow = (const TA *) p.A + (int64_t) (wm * 32 + lrow) * K + (lane >> 5) * 8;
+        static_for<NAF>([&](auto f) { af[f] = *(const u32x4 *) (arow + f * 16); });
+    }
+
+    auto origin = [&](int t, int &b, int &y0, int &x0) {
+        x0 = (t % tiles_x) * TW;
+        const int q = t / tiles_x;
+        y0 = (q % tiles_y) * C::TH;
+        b = q / tiles_y;
+    };
+    u32x4 pf[PF];
+    auto prefetch = [&](int t) {
+        int b, y0, x0;
+        origin(t, b, y0, x0);
+        const TA *xb = (const TA *) p.X + (int64_t) b * p.x_bstride;
+        static_for<PF>([&](auto i) {
+            const int c = tid + i * NT;
+            pf[i] = u32x4{0u, 0u, 0u, 0u};
+            if (c < HCH) {
+                const int px = c / CPP, kc = c - px * CPP;
+                const int hy = px / HWD, hx = px - hy * HWD;
+                const int iy = y0 + hy - 1, ix = x0 + hx - 1;
+                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
+                    pf[i] = *(const u32x4 *) (xb + (int64_t) (iy * W + ix) * IC + kc * 8);
+            }
+        });
+    };
+    auto commit = [&]() {
+        static_for<PF>([&](auto i) {
+            const int c = tid + i * NT;
+            if (c < HCH) {
+                const int px = c / CPP, kc = c - px * CPP;
+                *(u32x4 *) (smem + px * ROWB + kc * 16) = pf[i];
+            }
+        });
+    };
+
+    int t = (int) blockIdx.x;
+    if (t < ntiles) prefetch(t);
+    for (; t < ntiles; t += (int) gridDim.x) {
+        commit();
+        __syncthreads();
+        if (t + (int) gridDim.x < ntiles) prefetch(t + (int) gridDim.x);  // lands during the MFMAs
+
+        floatx16 acc[TN];
+#pragma unroll
+        for (int b = 0; b < TN; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[b][v] = 0.0f;
+        static_for<9>([&](auto tap_c) {
+            constexpr int tap = decltype(tap_c)::value;
+            constexpr int dy = tap / 3 - 1, dx = tap % 3 - 1;
+            static_for<KS>([&](auto ks_c) {
+                constexpr int ks = decltype(ks_c)::value;
+#pragma unroll
+                for (int b = 0; b < TN; b++) {
+                    const int hy = wn * TN + b + dy + 1;
+                    const u32x4 bf = *(const u32x4 *) (smem + (hy * HWD + lrow + dx + 1) * ROWB + ks * 32 + lk);
+                    mfma_op<TA>::run(af[tap * KS + ks], bf, acc[b]);
+                }
+            });
+        });
+
+        int b0, y0, x0;
+        origin(t, b0, y0, x0);
+        const int n0 = (b0 * H + y0) * W + x0;  // top-left pixel of the tile
+        if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+            for (int b = 0; b < TN; b++) {
+                const int n = n0 + (wn * TN + b) * W + lrow;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = wm * 32 + i * 8 + (lane >> 5) * 4;
+                    const float q[4] = {acc[b][i * 4], acc[b][i * 4 + 1], acc[b][i * 4 + 2], acc[b][i * 4 + 3]};
+                    epi_store_quad<TO, MODE>(p, q, m, n);
+                }
+            }
+            __syncthreads();  // halo reads done before the next commit
+        } else {
+            __syncthreads();  // halo reads done: the LDS becomes the tail's
+            constexpr int SOS = tile_tail_lds<M, C::BN>::SOS;
+            float *so = (float *) smem;
+#pragma unroll
+            for (int b = 0; b < TN; b++) {
+                const int col = (wn * TN + b) * TW + lrow;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = wm * 32 + i * 8 + (lane >> 5) * 4;
+                    const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) b0 * p.OC + row);
+                    const floatx4 bb = *(const floatx4 *) (p.bias + row);
+                    floatx4 v;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) v[j] = leaky(acc[b][i * 4 + j] * id[j] + bb[j]);
+                    *(floatx4 *) (so + col * SOS + row) = v;
+                }
+            }
+            tile_tail<TA, TT, M, C::BN, NT>(ta, so, n0, TW, tid);
+            __syncthreads();  // tail's LDS reads done before the next commit
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+bool modconv_halo_ok(bool f16, int mode, int IC, int OC, int H, int W, bool tail) {
+    const int M = mode == MODE_DENSE ? OC : 4 * OC;
+    if (!f16 || (IC != 32 && IC != 64) || (M != 32 && M != 64 && M != 128)) return false;
+    // with the stage tail the A fragments keep one workgroup per CU, and the
+    // tail's gather latency is then exposed: those stages use k_conv.hip
+    if (tail) return false;
+    if (mode == MODE_SUBPIX && M != 128) return false;
+    const int th = (M == 128 || (IC == 64 && tail)) ? 4 : 8;  // halo_cfg::TH
+    return W % 32 == 0 && H % th == 0;
+}
+
+static int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
+
+template <int IC, int M, int MODE, int EPI, typename TO, typename TT>
+static hipError_t launch_halo_k(const ConvParams &p, const TailArgs &ta, hipStream_t st) {
+    typedef halo_cfg<IC, M, EPI> C;
+    const int tiles_x = p.W / C::TW, tiles_y = p.H / C::TH;
+    const int nframes = p.N / (p.H * p.W);
+    const int ntiles = tiles_x * tiles_y * nframes;
+    auto kern = modconv_halo_kernel<IC, M, MODE, EPI, TO, TT>;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, C::NT, 0) != hipSuccess || occ < 1) occ = 1;
+    int grid = cu_count() * occ;
+    if (grid > ntiles) grid = ntiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned) grid), dim3(C::NT), 0, st, p, ta, tiles_x, tiles_y, ntiles);
+    return hipGetLastError();
+}
+
+template <int IC, int M, typename TO, typename TT>
+static hipError_t launch_halo_m(const ConvParams &p, int mode, bool tail, const TailArgs &ta,
+                                hipStream_t st) {
+    if (tail) {
+        if constexpr (M <= 64) return launch_halo_k<IC, M, MODE_DENSE, EPI_TAIL, TO, TT>(p, ta, st);
+        return hipErrorInvalidValue;
+    }
+    if (mode == MODE_DENSE) return launch_halo_k<IC, M, MODE_DENSE, EPI_STORE, TO, TT>(p, ta, st);
+    if constexpr (M == 128) return launch_halo_k<IC, M, MODE_SUBPIX, EPI_STORE, TO, TT>(p, ta, st);
+    return hipErrorInvalidValue;
+}
+
+template <typename TO, typename TT>
+static hipError_t launch_halo_t(const ConvParams &p, int mode, bool tail, const TailArgs &ta,
+                                hipStream_t st) {
+    const int M = p.M;
+    if (p.IC == 32) {
+        if (M == 32) return launch_halo_m<32, 32, TO, TT>(p, mode, tail, ta, st);
+        if (M == 64) return launch_halo_m<32, 64, TO, TT>(p, mode, tail, ta, st);
+        return launch_halo_m<32, 128, TO, TT>(p, mode, tail, ta, st);
+    }
+    if (M == 32) return launch_halo_m<64, 32, TO, TT>(p, mode, tail, ta, st);
+    if (M == 64) return launch_halo_m<64, 64, TO, TT>(p, mode, tail, ta, st);
+    return launch_halo_m<64, 128, TO, TT>(p, mode, tail, ta, st);
+}
+
+// f16 operands; out_f16: stored activation type (EPI_STORE); tail: fused
+// stage tail with an f16 (trunk_f16) or f32 trunk
+hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, const TailArgs *tail,
+                               bool trunk_f16, hipStream_t st) {
+    if (tail) {
+        if (trunk_f16) return launch_halo_t<float, half_t>(p, mode, true, *tail, st);
+        return launch_halo_t<float, float>(p, mode, true, *tail, st);
+    }
+    const TailArgs none{};
+    if (out_f16) return launch_halo_t<half_t, half_t>(p, mode, false, none, st);
+    return launch_halo_t<float, half_t>(p, mode, false, none, st);
+}
+
+}  // namespace tpmd

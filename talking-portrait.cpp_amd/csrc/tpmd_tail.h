@@ -192,8 +192,12 @@ struct tile_tail_lds {
     static constexpr int FLOATS = WFS0 + 3 * C;
 };
 
+// The tile's pixels: p = 0..BN-1 -> frame pixel pix0 + p (tw = 0: a run of
+// consecutive pixels starting at batch pixel n0) or pix0 + (p / tw) * r +
+// p % tw (tw > 0: a tw-wide block of rows whose top-left pixel is n0).  Every
+// pixel of the tile exists (the caller's tiling guarantees it).
 template <typename TF, typename TT, int C, int BN, int NT>
-__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int N, int tid) {
+__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int tw, int tid) {
 #pragma clang fp contract(off)
     typedef tile_tail_lds<C, BN> L;
     constexpr int G = C / 8;
@@ -203,6 +207,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
     const int r = a.r, rh = r >> 1;
     const int RR = r * r;
     const int fr = n0 / RR;                          // the tile lies in one frame
+    const int pix0 = n0 - fr * RR;
+    auto pix_of = [&](int p) { return tw ? pix0 + (p / tw) * r + p % tw : pix0 + p; };
     float *so = lds, *prm = lds + L::PRM0, *wfs = lds + L::WFS0;
 
     // folded ToFlow weights of this frame (gemm_weight: W * s rounded to f32)
@@ -215,8 +221,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
     // ---- phase 1: one thread per pixel
     if (tid < BN) {
         const int p = tid;
-        const int n = n0 + p < N ? n0 + p : N - 1;
-        const int pix = n - fr * RR;
+        const int pix = pix_of(p);
         const int y = pix / r, x = pix - y * r;
         float fl[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -238,7 +243,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
                 fl[k] = fl[k] + upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
             if (a.rgb_prev) up[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
         }
-        if (a.flow_cur && n0 + p < N) {
+        if (a.flow_cur) {
 #pragma unroll
             for (int k = 0; k < 3; k++) a.flow_cur[((int64_t) fr * 3 + k) * RR + pix] = fl[k];
         }
@@ -262,8 +267,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
     const TF *feat = (const TF *) a.feat;
     for (int lp0 = 0; lp0 < BN; lp0 += PPB) {
         const int lp = lp0 + wid * PPW + grp;
-        const int n = n0 + lp;
-        const bool valid = n < N;
+        const int pix = pix_of(lp);
+        const int64_t pp = (int64_t) fr * RR + pix;
         const floatx4 q0 = *(const floatx4 *) (prm + lp * L::PRM);
         const floatx4 q1 = *(const floatx4 *) (prm + lp * L::PRM + 4);
         taps4 t;
@@ -304,9 +309,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
             warp[e] = smp[e] * m;
             trunk[e] = warp[e] + ov[e] * one_m;
         }
-        const int64_t pp = valid ? n : N - 1;
-        if (valid && a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
-        if (valid && a.trunk) {
+        if (a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
+        if (a.trunk) {
             if (a.s_next) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
@@ -321,13 +325,12 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
             for (int e = 0; e < 8; e++) acc = __builtin_fmaf(wr[k][e], warp[e], acc);
             rgb[k] = group_sum<G>(acc);
         }
-        if (valid && gl < 3) {
+        if (gl < 3) {
             const int k = gl;
             const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
             float v = leaky(rv + a.rlb[k]);
             v = v + a.rbias[k];
             if (a.rgb_prev) v = v + (k == 0 ? q1[1] : (k == 1 ? q1[2] : q1[3]));
-            const int pix = n - fr * RR;
             a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
         }
     }

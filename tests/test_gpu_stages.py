@@ -142,7 +142,7 @@ def test_conv_tail_all_stages(om, torch_cuda, ftype, ic, oc):
     nf = lat.shape[0]
     for j in range(len(oc)):
         r, C = 8 << j, oc[j]
-        if r * r * C * nf > (1 << 23) and j < len(oc) - 1:
+        if r * r * C * nf > (1 << 24) and j < len(oc) - 1:
             continue                                      # keep the oracle side quick
         base = f"dec.convs.{2 * j + 1}"
         c1 = g.standard_normal((nf, r * r, C)).astype(np.float32)
