@@ -22,6 +22,33 @@ sys.path[:0] = [ROOT, PKG]
 PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}
 REF_FPS_RTX5070TI = 213.2   # mdec, GGML-CUDA f16 fast graph (docs/vulkan-perf.md:134,143)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+COPY_PROBE_BYTES = 256 << 20   # the calibration copy: reads and writes this many bytes
+
+
+def measured_traffic(stage):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (rows `| stage | fetch KiB | write KiB | ... | bytes |`),
+    or None when that stage has no row"""
+    try:
+        for line in open(TRAFFIC_FILE):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 6 and cells[0] == stage:
+                return int(float(cells[-1]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe():
+    """a plain device copy of COPY_PROBE_BYTES, the reference kernel that
+    scales the FETCH_SIZE / WRITE_SIZE counters to bytes"""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def fused_tail(oc, r):
@@ -109,6 +136,8 @@ def main():
     ap.add_argument("--ftype", default="f16", choices=["f16", "f32"])
     ap.add_argument("--workload", default="iid", choices=["iid", "smooth", "stress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run the 256 MiB calibration copy (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -163,7 +192,7 @@ def main():
     dom = max(range(len(stages)), key=lambda i: stages[i]["us"])
     r = dict(stages[dom])
     r["kernel"] = r.pop("name")
-    r["traffic"] = None
+    r["traffic"] = measured_traffic(r["kernel"])
     r.pop("us")
 
     out = {
@@ -187,6 +216,8 @@ def main():
         "stages": stages,
         "stage_sum_us": round(float(us.sum()), 1),
     }
+    if args.copy_probe:
+        copy_probe()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
