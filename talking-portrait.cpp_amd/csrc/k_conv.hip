@@ -238,7 +238,7 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, T
                 }
             }
         }
-        tile_tail<TF, TT, BM, BN, NT>(ta, so, n0, 0, tid);
+        tile_tail<TF, TT, BM, BN, NT, 0>(ta, so, n0, tid);
     }
 }
 
@@ -319,8 +319,10 @@ int64_t modconv_ws_elems(int mode, int nframes, int H, int W, int IC, int OC, bo
 }
 
 template <typename TA, typename TO, int BM, int BN, int WM, int WN, int RB, typename TF, typename TT>
-static hipError_t launch_rb(const ConvParams &p, int mode, int epi, int nsplit, const TailArgs &ta,
+static hipError_t launch_rb(ConvParams p, int mode, int epi, int nsplit, const TailArgs &ta,
                             hipStream_t st) {
+    p.T = 9 * p.IC * (int) sizeof(TA) / RB;  // k tiles of this row width
+    if (nsplit > p.T) return hipErrorInvalidValue;
     const int ntile = p.MT * ((p.N + BN - 1) / BN);
     dim3 grid((unsigned) ntile, (unsigned) nsplit);
     dim3 block(WM * WN * 64);
@@ -343,7 +345,12 @@ static hipError_t launch_rb(const ConvParams &p, int mode, int epi, int nsplit, 
 template <typename TA, typename TO, int BM, int BN, int WM, int WN, typename TF, typename TT>
 static hipError_t launch_cfg(const ConvParams &p, int mode, int epi, int nsplit, const TailArgs &ta,
                              hipStream_t st) {
-    if (row_bytes(p.IC, (int) sizeof(TA)) == 128)
+    // fused-tail convs with IC <= 64 keep 64-byte k rows: the smaller LDS
+    // footprint lets more workgroups share a CU, which hides the tail's
+    // gather latency (measured faster at 256 x 256; at IC = 128 the wider
+    // rows win)
+    const bool narrow = epi == EPI_TAIL && p.IC * (int) sizeof(TA) <= 128;
+    if (!narrow && row_bytes(p.IC, (int) sizeof(TA)) == 128)
         return launch_rb<TA, TO, BM, BN, WM, WN, 128, TF, TT>(p, mode, epi, nsplit, ta, st);
     return launch_rb<TA, TO, BM, BN, WM, WN, 64, TF, TT>(p, mode, epi, nsplit, ta, st);
 }
@@ -353,7 +360,6 @@ static hipError_t launch_typed(ConvParams p, int mode, int epi, int nsplit, cons
                                hipStream_t st) {
     const TileCfg tc = pick_tile(p.M, epi == EPI_TAIL);
     p.MT = p.M / tc.bm;
-    p.T = 9 * p.IC * (int) sizeof(TA) / row_bytes(p.IC, (int) sizeof(TA));
     if (tc.bm == 128 && tc.bn == 128)
         return launch_cfg<TA, TO, 128, 128, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
     if (tc.bm == 64 && tc.bn == 128)

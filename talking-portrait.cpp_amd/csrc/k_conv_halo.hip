@@ -105,12 +105,19 @@ __global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArg
         });
     };
 
-    int t = (int) blockIdx.x;
-    if (t < ntiles) prefetch(t);
-    for (; t < ntiles; t += (int) gridDim.x) {
+    // workgroup ids reach the 8 XCDs round robin: the workgroups of one XCD
+    // walk one contiguous range of tiles, so neighbouring tiles share an L2
+    const int G = (int) gridDim.x;
+    const int xcd = (int) blockIdx.x & 7, slot = (int) blockIdx.x >> 3;
+    const int nx = (G - xcd + 7) >> 3;                      // workgroups on this XCD
+    const int per = (ntiles + 7) >> 3;                      // tiles per XCD
+    const int tbeg = xcd * per, tend = tbeg + per < ntiles ? tbeg + per : ntiles;
+    int t = tbeg + slot;
+    if (t < tend) prefetch(t);
+    for (; t < tend; t += nx) {
         commit();
         __syncthreads();
-        if (t + (int) gridDim.x < ntiles) prefetch(t + (int) gridDim.x);  // lands during the MFMAs
+        if (t + nx < tend) prefetch(t + nx);  // lands during the MFMAs
 
         floatx16 acc[TN];
 #pragma unroll
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArg
                     *(floatx4 *) (so + col * SOS + row) = v;
                 }
             }
-            tile_tail<TA, TT, M, C::BN, NT>(ta, so, n0, TW, tid);
+            tile_tail<TA, TT, M, C::BN, NT, TW>(ta, so, n0, tid);
             __syncthreads();  // tail's LDS reads done before the next commit
         }
     }

@@ -192,12 +192,12 @@ struct tile_tail_lds {
     static constexpr int FLOATS = WFS0 + 3 * C;
 };
 
-// The tile's pixels: p = 0..BN-1 -> frame pixel pix0 + p (tw = 0: a run of
-// consecutive pixels starting at batch pixel n0) or pix0 + (p / tw) * r +
-// p % tw (tw > 0: a tw-wide block of rows whose top-left pixel is n0).  Every
+// The tile's pixels: p = 0..BN-1 -> frame pixel pix0 + p (TWC = 0: a run of
+// consecutive pixels starting at batch pixel n0) or pix0 + (p / TWC) * r +
+// p % TWC (TWC > 0: a TWC-wide block of rows whose top-left pixel is n0).  Every
 // pixel of the tile exists (the caller's tiling guarantees it).
-template <typename TF, typename TT, int C, int BN, int NT>
-__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int tw, int tid) {
+template <typename TF, typename TT, int C, int BN, int NT, int TWC>
+__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int tid) {
 #pragma clang fp contract(off)
     typedef tile_tail_lds<C, BN> L;
     constexpr int G = C / 8;
@@ -208,7 +208,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
     const int RR = r * r;
     const int fr = n0 / RR;                          // the tile lies in one frame
     const int pix0 = n0 - fr * RR;
-    auto pix_of = [&](int p) { return tw ? pix0 + (p / tw) * r + p % tw : pix0 + p; };
+    auto pix_of = [&](int p) { return TWC ? pix0 + (p / (TWC ? TWC : 1)) * r + p % (TWC ? TWC : 1) : pix0 + p; };
     float *so = lds, *prm = lds + L::PRM0, *wfs = lds + L::WFS0;
 
     // folded ToFlow weights of this frame (gemm_weight: W * s rounded to f32)
