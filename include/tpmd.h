@@ -79,6 +79,22 @@ int tpmd_set_weight(tpmd_ctx *ctx, const char *name, const float *data, int64_t 
  * (src/motion_dec.cpp:17-29). */
 const char *tpmd_weight_name(const tpmd_ctx *ctx, int i, int64_t *n, int *is_matrix);
 
+/* Hand every decoder tensor of a motion_ae GGUF v3 checkpoint
+ * (motion_ae_{f32,f16}.gguf, general.architecture "float-motion-ae") to the
+ * context, as tpmd_set_weight does: replaces weights_t::load for the dec.*
+ * tensors (src/gguf_load.cpp:51-197, src/tp.cpp:33-35).  Tensors the file
+ * lacks are reported by tpmd_prepare ("missing tensor <name>").  Returns 0,
+ * or -1 with the reason (file defects as the reference words them: "not a
+ * GGUF file", "unsupported GGUF version", "unexpected architecture", "tensor
+ * <name> out of bounds", ...) in err[0..err_size). */
+int tpmd_load_gguf(tpmd_ctx *ctx, const char *path, char *err, size_t err_size);
+/* One tensor of a GGUF v3 file as f32 (F16 tensors widened exactly);
+ * *is_f16 = stored as F16.  out may be NULL to query the element count.
+ * Returns the element count, or -1 with the reason in err.  Needs no
+ * device. */
+int64_t tpmd_gguf_read_tensor(const char *path, const char *name, float *out, int64_t cap,
+                              int *is_f16, char *err, size_t err_size);
+
 /* motion_dec::prepare (src/motion_dec.h:38, src/motion_dec.cpp:31-226):
  * S_aug demodulation Gram rows, composed sub-pixel up-conv kernels, cf GEMM
  * matrices; uploads every derived tensor.  Fails naming the first missing

@@ -12,7 +12,11 @@
 // Output file: f32 frames [n_frames][3][R][R], then the single-frame decode
 // of frame 0 [3][R][R].  Exit status 0 on success; errors on stderr.
 //
-//   shim_check <blob> <out> [device]
+//   shim_check <blob> <out> [device] [gguf]
+//
+// With a GGUF path the weights come from that checkpoint through
+// tp::gguf_weight_source (the reference's tp_load flow, src/tp.cpp:13-41)
+// and the blob's weight section is ignored.
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -20,6 +24,7 @@
 #include <string>
 #include <vector>
 
+#include "gguf.h"
 #include "motion_dec.h"
 
 namespace {
@@ -74,7 +79,7 @@ struct no_taps {
 
 int main(int argc, char **argv) {
     if (argc < 3) {
-        fprintf(stderr, "usage: shim_check <blob> <out> [device]\n");
+        fprintf(stderr, "usage: shim_check <blob> <out> [device] [gguf]\n");
         return 2;
     }
     reader r;
@@ -132,6 +137,16 @@ int main(int argc, char **argv) {
     tp::motion_dec dec;
     dec.w = &w;
     std::string err;
+    tp::gguf_file gf;
+    tp::gguf_weight_source gw;
+    if (argc > 4) {
+        if (!gf.open(argv[4], "float-motion-ae", err)) {
+            fprintf(stderr, "shim_check: %s\n", err.c_str());
+            return 1;
+        }
+        gw.f = &gf;
+        dec.w = &gw;
+    }
     if (!dec.prepare(be, err) || !dec.build(be, false, err) || !dec.set_feats(m, err)) {
         fprintf(stderr, "shim_check: %s\n", err.c_str());
         return 1;

@@ -52,6 +52,8 @@ def lib():
             "tpmd_last_error": (C, [P]),
             "tpmd_set_weight": (I, [P, C, P, I64, I]),
             "tpmd_weight_name": (C, [P, I, P, P]),
+            "tpmd_load_gguf": (I, [P, C, P, ctypes.c_size_t]),
+            "tpmd_gguf_read_tensor": (I64, [C, C, P, I64, P, P, ctypes.c_size_t]),
             "tpmd_prepare": (I, [P]),
             "tpmd_build": (I, [P, I]),
             "tpmd_batch": (I, [P]),
@@ -169,6 +171,12 @@ class MotionDecoder:
             out.append((nm.decode(), n.value, bool(m.value)))
             i += 1
 
+    def load_gguf(self, path):
+        """every decoder tensor of a motion_ae GGUF file (tpmd_load_gguf)"""
+        err = ctypes.create_string_buffer(512)
+        if lib().tpmd_load_gguf(self.h, str(path).encode(), err, len(err)) != 0:
+            raise TpmdError(err.value.decode())
+
     def set_weights(self, raw):
         for name, (arr, f16) in raw.items():
             self.set_weight(name, arr, f16_file=f16)
@@ -243,6 +251,21 @@ class MotionDecoder:
         self._check(lib().tpmd_stage_conv_tail(self.h, j, _ptr(c1), n, _ptr(s_conv), _ptr(s_flow),
                                                _ptr(flow_prev), _ptr(rgb_prev), _ptr(flow), _ptr(trunk),
                                                _ptr(rgb), _ptr(warp), _stream(stream)))
+
+
+def gguf_read_tensor(path, name):
+    """(float32 array, stored_as_f16) of one tensor of a GGUF file (no device)"""
+    err = ctypes.create_string_buffer(512)
+    f16 = ctypes.c_int()
+    n = lib().tpmd_gguf_read_tensor(str(path).encode(), name.encode(), None, 0, ctypes.byref(f16), err,
+                                    len(err))
+    if n < 0:
+        raise TpmdError(err.value.decode())
+    out = np.empty(n, np.float32)
+    if lib().tpmd_gguf_read_tensor(str(path).encode(), name.encode(), _hptr(out), n, ctypes.byref(f16), err,
+                                   len(err)) < 0:
+        raise TpmdError(err.value.decode())
+    return out, bool(f16.value)
 
 
 # ---- op level (torch cuda tensors)
