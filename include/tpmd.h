@@ -123,6 +123,25 @@ int tpmd_set_feats_device(tpmd_ctx *ctx, const float *const *feats_dev);
  * (on_device = 0, synchronous like the reference) or device pointers
  * (on_device = 1; enqueued on the decoder's stream, see tpmd_sync). */
 int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, int on_device);
+/* Frame output path of a clip (the generation loop's decode stage,
+ * src/pipeline.cpp:160-185): n_frames latents (host [n][512]) are decoded
+ * in launches of `batch` frames; while launch k runs, the frames of launch
+ * k-1 come back over a second stream into pinned staging and are handed
+ * over.  format TPMD_FRAME_F32: [3][R][R] f32 per frame, as decode_batch;
+ * TPMD_FRAME_RGB24: [R][R][3] u8 per frame, converted on the GPU with the
+ * video writer's rule (tools/tp-cli.cpp:43-53: clamp to [-1,1],
+ * (v+1)/2*255, truncate), a quarter of the bytes.  out: host buffer for all
+ * frames, or NULL; cb: called per frame in order with the frame (valid only
+ * during the call, tp_frame_cb semantics, include/tp.h:57-62), or NULL;
+ * a nonzero return stops decoding.  Returns n_frames (also when stopped, as
+ * generate_impl does) or -1.  The first call allocates two slots of device
+ * and pinned host memory for `batch` frames, kept by the context. */
+#define TPMD_FRAME_F32 0
+#define TPMD_FRAME_RGB24 1
+typedef int (*tpmd_frame_cb)(int64_t frame_idx, const void *frame, void *ud);
+int64_t tpmd_decode_frames(tpmd_ctx *ctx, const float *styles, int64_t n_frames, int format, void *out,
+                           tpmd_frame_cb cb, void *ud);
+
 /* motion_dec::decode (src/motion_dec.h:44-45, :1162-1188): one frame. */
 int tpmd_decode(tpmd_ctx *ctx, const float *style, float *img);
 /* wait for work enqueued by on_device calls */
@@ -191,6 +210,9 @@ int tpmd_gather(const void *feat, int feat_f16, int C, int W, int H, const float
  * y0 = floor(fy), wx = fx - x0, wy = fy - y0 per point (device pointers) */
 int tpmd_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0,
                      int32_t *y0, float *wx, float *wy, void *stream);
+/* n CHW f32 frames [n][3][R][R] -> [n][R][R][3] u8 with the video writer's
+ * conversion (tools/tp-cli.cpp:43-53); device pointers, R*R % 4 == 0 */
+int tpmd_frames_to_rgb24(const float *chw, int n, int R, uint8_t *rgb, void *stream);
 /* GGML_OP_UPFIRDN2X (patch :128-134, :996-1045): SP [CB][H][W] -> [CB][2H][2W] */
 int tpmd_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB,
                    void *stream);

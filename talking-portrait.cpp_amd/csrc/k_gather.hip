@@ -135,6 +135,38 @@ __global__ __launch_bounds__(256) void flow_grid_kernel(const float *__restrict_
     }
 }
 
+// CHW f32 frames in [-1, 1] -> interleaved 8-bit RGB, the video writer's
+// conversion (tools/tp-cli.cpp:43-53): clamp to [-1, 1], (v + 1) / 2 * 255,
+// truncated toward zero.  Four pixels per thread: float4 reads of each
+// plane, three 32-bit stores of the 12 interleaved bytes.
+__global__ __launch_bounds__(256) void rgb24_kernel(const float *__restrict__ chw,
+                                                    uint8_t *__restrict__ rgb, int n, int R) {
+#pragma clang fp contract(off)
+    const int64_t quads = (int64_t) R * R / 4;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < quads * n;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t f = i / quads, q = i - f * quads;
+        const float *src = chw + f * 3 * (int64_t) R * R + q * 4;
+        uint8_t b[12];
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            const floatx4 v = *(const floatx4 *) (src + (int64_t) c * R * R);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float x = v[e];
+                x = x < -1.0f ? -1.0f : (x > 1.0f ? 1.0f : x);
+                b[e * 3 + c] = (uint8_t) ((x + 1.0f) / 2.0f * 255.0f);
+            }
+        }
+        uint32_t w[3];
+        __builtin_memcpy(w, b, 12);
+        uint32_t *dst = (uint32_t *) (rgb + (f * (int64_t) R * R + q * 4) * 3);
+        dst[0] = w[0];
+        dst[1] = w[1];
+        dst[2] = w[2];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 
@@ -200,6 +232,13 @@ hipError_t launch_upfirdn2x(const float *x, const float *k4, float *y, int W, in
     if (CB <= 0 || W <= 0 || H <= 0) return hipSuccess;
     hipLaunchKernelGGL(upfirdn2x_kernel, dim3(grid_for(4 * (int64_t) W * H * CB, 256)), dim3(256),
                        0, st, x, k4, y, W, H, CB);
+    return hipGetLastError();
+}
+
+hipError_t launch_rgb24(const float *chw, int n, int R, uint8_t *rgb, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rgb24_kernel, dim3(grid_for((int64_t) n * R * R / 4, 256)), dim3(256), 0, st, chw, rgb,
+                       n, R);
     return hipGetLastError();
 }
 

@@ -107,6 +107,15 @@ struct tpmd_ctx {
     size_t scr_sz[4] = {};
 
     bool profile = false;
+
+    // frame streaming (tpmd_decode_frames): two device frame slots, pinned
+    // host staging, a copy stream and events; made by the first call
+    struct {
+        hipStream_t copy = nullptr;
+        hipEvent_t computed[2] = {}, copied[2] = {};
+        void *dev[2] = {}, *host[2] = {};
+        size_t bytes = 0;  // per slot
+    } fs;
     std::vector<hipEvent_t> ev;
     std::vector<float> times;
 
@@ -182,6 +191,13 @@ struct tpmd_ctx {
         for (void *p : batch_allocs) (void) hipFree(p);
         for (void *p : scr)
             if (p) (void) hipFree(p);
+        for (int i = 0; i < 2; i++) {
+            if (fs.dev[i]) (void) hipFree(fs.dev[i]);
+            if (fs.host[i]) (void) hipHostFree(fs.host[i]);
+            if (fs.computed[i]) (void) hipEventDestroy(fs.computed[i]);
+            if (fs.copied[i]) (void) hipEventDestroy(fs.copied[i]);
+        }
+        if (fs.copy) (void) hipStreamDestroy(fs.copy);
         if (own_stream) (void) hipStreamDestroy(own_stream);
     }
 };
@@ -813,6 +829,95 @@ int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int 
     return 0;
 }
 
+// slot buffers of the frame stream, grow-only
+static bool frame_slots(tpmd_ctx *c, size_t bytes) {
+    auto &f = c->fs;
+    if (!f.copy) {
+        if (!c->hip_ok(hipStreamCreateWithFlags(&f.copy, hipStreamNonBlocking), "copy stream")) return false;
+        for (int i = 0; i < 2; i++)
+            if (!c->hip_ok(hipEventCreateWithFlags(&f.computed[i], hipEventDisableTiming), "event") ||
+                !c->hip_ok(hipEventCreateWithFlags(&f.copied[i], hipEventDisableTiming), "event"))
+                return false;
+    }
+    if (f.bytes >= bytes) return true;
+    for (int i = 0; i < 2; i++) {
+        if (f.dev[i]) (void) hipFree(f.dev[i]);
+        if (f.host[i]) (void) hipHostFree(f.host[i]);
+        f.dev[i] = f.host[i] = nullptr;
+    }
+    f.bytes = 0;
+    for (int i = 0; i < 2; i++) {
+        if (!c->hip_ok(hipMalloc(&f.dev[i], bytes), "frame slot") ||
+            !c->hip_ok(hipHostMalloc(&f.host[i], bytes, hipHostMallocDefault), "pinned frame slot"))
+            return false;
+    }
+    f.bytes = bytes;
+    return true;
+}
+
+int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, int format, void *out,
+                           tpmd_frame_cb cb, void *ud) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built || !c->feats_set) {
+        c->err = !c->built ? "decoder not built" : "feats not set";
+        return -1;
+    }
+    if (!styles || n_frames < 1 || (format != TPMD_FRAME_F32 && format != TPMD_FRAME_RGB24)) {
+        c->err = "tpmd_decode_frames: bad arguments";
+        return -1;
+    }
+    const size_t R = (size_t) c->out_res();
+    const size_t fsz = format == TPMD_FRAME_F32 ? 3 * R * R * 4 : 3 * R * R;
+    const int B = c->batch;
+    if (!frame_slots(c, (size_t) B * fsz)) return -1;
+    const bool prof = c->profile;
+    c->profile = false;  // no per-stage events inside the stream
+    auto &f = c->fs;
+    const int64_t nb = (n_frames + B - 1) / B;
+    bool ok = true, stopped = false;
+    // frames of batch k, from its pinned slot, to the caller
+    auto deliver = [&](int64_t k) {
+        const int s = (int) (k & 1);
+        const int64_t t0 = k * B;
+        const int64_t nk = std::min<int64_t>(B, n_frames - t0);
+        if (!c->hip_ok(hipEventSynchronize(f.copied[s]), "frame copy")) return ok = false;
+        const char *src = (const char *) f.host[s];
+        if (out) memcpy((char *) out + (size_t) t0 * fsz, src, (size_t) nk * fsz);
+        if (cb)
+            for (int64_t i = 0; i < nk; i++)
+                if (cb(t0 + i, src + (size_t) i * fsz, ud)) return !(stopped = true);
+        return true;
+    };
+    for (int64_t k = 0; k < nb && ok && !stopped; k++) {
+        const int s = (int) (k & 1);
+        const int64_t t0 = k * B;
+        const int nk = (int) std::min<int64_t>(B, n_frames - t0);
+        // slot s is free once the copy of batch k-2 has finished
+        if (k >= 2 && !c->hip_ok(hipStreamWaitEvent(c->stream, f.copied[s], 0), "wait")) ok = false;
+        ok = ok && c->hip_ok(hipMemcpyAsync(c->lat, styles + (size_t) t0 * 512, (size_t) nk * 512 * 4,
+                                            hipMemcpyHostToDevice, c->stream),
+                             "style upload");
+        if (format == TPMD_FRAME_F32) {
+            ok = ok && enqueue_decode(c, nk, (float *) f.dev[s]);
+        } else {
+            ok = ok && enqueue_decode(c, nk, c->img) &&
+                 c->hip_ok(launch_rgb24(c->img, nk, (int) R, (uint8_t *) f.dev[s], c->stream), "rgb24");
+        }
+        ok = ok && c->hip_ok(hipEventRecord(f.computed[s], c->stream), "event") &&
+             c->hip_ok(hipStreamWaitEvent(f.copy, f.computed[s], 0), "wait") &&
+             c->hip_ok(hipMemcpyAsync(f.host[s], f.dev[s], (size_t) nk * fsz, hipMemcpyDeviceToHost, f.copy),
+                       "frame download") &&
+             c->hip_ok(hipEventRecord(f.copied[s], f.copy), "event");
+        if (ok && k >= 1) deliver(k - 1);  // batch k decodes while batch k-1 is handed over
+        if (ok && !stopped && k == nb - 1) deliver(k);
+    }
+    // leave both streams idle: the slots may be reused by the next call
+    const bool drained = c->hip_ok(hipStreamSynchronize(f.copy), "drain") &&
+                         c->hip_ok(hipStreamSynchronize(c->stream), "drain");
+    c->profile = prof;
+    return ok && drained ? n_frames : -1;
+}
+
 int tpmd_decode(tpmd_ctx *c, const float *style, float *img) {
     return tpmd_decode_batch(c, style, 1, img, 0);
 }
@@ -1036,6 +1141,13 @@ int tpmd_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int
     if (!grid || !x0 || !y0 || !wx || !wy) return -1;
     return launch_gather_taps(grid, W, H, N, planar, x0, y0, wx, wy, (hipStream_t) stream) == hipSuccess ? 0
                                                                                                       : -1;
+}
+
+int tpmd_frames_to_rgb24(const float *chw, int n, int R, uint8_t *rgb, void *stream) {
+    if (n < 0 || R < 1 || (R * R) % 4 != 0) return -1;
+    if (n == 0) return 0;
+    if (!chw || !rgb) return -1;
+    return launch_rgb24(chw, n, R, rgb, (hipStream_t) stream) == hipSuccess ? 0 : -1;
 }
 
 int tpmd_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB, void *stream) {

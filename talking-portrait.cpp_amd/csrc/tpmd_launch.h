@@ -54,6 +54,8 @@ hipError_t launch_gather_taps(const float *grid, int W, int H, int64_t N, int pl
                               int32_t *y0, float *wx, float *wy, hipStream_t st);
 hipError_t launch_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int64_t CB,
                             hipStream_t st);
+// CHW f32 frames -> interleaved RGB24 (tp-cli's conversion)
+hipError_t launch_rgb24(const float *chw, int n, int R, uint8_t *rgb, hipStream_t st);
 hipError_t launch_flow_grid(const float *fl, const float *xs, float *y, int64_t N,
                             hipStream_t st);
 

@@ -29,6 +29,9 @@ HEADER = os.path.join(os.path.dirname(_HERE), "include", "tpmd.h")
 
 W_F16_FILE = 1
 W_FOLDED = 2
+FRAME_F32 = 0
+FRAME_RGB24 = 1
+FRAME_CB = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p)
 
 
 class TpmdError(RuntimeError):
@@ -62,6 +65,8 @@ def lib():
             "tpmd_set_feats_device": (I, [P, P]),
             "tpmd_decode_batch": (I, [P, P, I, P, I]),
             "tpmd_decode": (I, [P, P, P]),
+            "tpmd_decode_frames": (I64, [P, P, I64, I, P, P, P]),
+            "tpmd_frames_to_rgb24": (I, [P, I, I, P, P]),
             "tpmd_sync": (I, [P]),
             "tpmd_set_stream": (I, [P, P]),
             "tpmd_profile_stages": (I, [P, I]),
@@ -212,6 +217,26 @@ class MotionDecoder:
         n = styles_dev.shape[0]
         self._check(lib().tpmd_decode_batch(self.h, _ptr(styles_dev), n, _ptr(imgs_dev), 1))
 
+    def decode_frames(self, styles, fmt=FRAME_F32, to_buffer=True, cb=None):
+        """a clip of latents (n, 512) through tpmd_decode_frames: returns the
+        frames array (n, 3, R, R) f32 or (n, R, R, 3) u8 when to_buffer, and
+        calls cb(index, frame_array) per frame (a truthy return stops)"""
+        s = np.ascontiguousarray(styles, dtype=np.float32).reshape(-1, 512)
+        n, R = s.shape[0], self.res
+        shape, dt = ((3, R, R), np.float32) if fmt == FRAME_F32 else ((R, R, 3), np.uint8)
+        out = np.empty((n,) + shape, dt) if to_buffer else None
+        nbytes = int(np.prod(shape)) * np.dtype(dt).itemsize
+
+        def tramp(idx, ptr, ud):
+            buf = (ctypes.c_char * nbytes).from_address(ptr)
+            return 1 if cb(idx, np.frombuffer(buf, dt).reshape(shape).copy()) else 0
+        c_cb = FRAME_CB(tramp) if cb else None
+        rc = lib().tpmd_decode_frames(self.h, _hptr(s), n, fmt, _hptr(out) if out is not None else None,
+                                      ctypes.cast(c_cb, ctypes.c_void_p) if c_cb else None, None)
+        if rc < 0:
+            raise TpmdError(self.last_error)
+        return out
+
     def decode(self, style):
         s = np.ascontiguousarray(style, dtype=np.float32).reshape(512)
         out = np.empty((3, self.res, self.res), np.float32)
@@ -298,6 +323,16 @@ def gather_taps(grid, W, H, planar=False, stream=None):
     if rc != 0:
         raise TpmdError("tpmd_gather_taps: invalid arguments")
     return x0, y0, wx, wy
+
+
+def frames_to_rgb24(chw, stream=None):
+    """(n, 3, R, R) f32 cuda frames -> (n, R, R, 3) uint8 (the video writer's rule)"""
+    import torch
+    n, _, R, _ = chw.shape
+    rgb = torch.empty((n, R, R, 3), dtype=torch.uint8, device=chw.device)
+    if lib().tpmd_frames_to_rgb24(_ptr(chw), n, R, _ptr(rgb), _stream(stream)) != 0:
+        raise TpmdError("tpmd_frames_to_rgb24: invalid arguments")
+    return rgb
 
 
 def upfirdn2x(x, k4, stream=None):
