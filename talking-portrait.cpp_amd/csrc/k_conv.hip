@@ -272,13 +272,16 @@ struct TileCfg {
     int bm, bn, wm, wn;
 };
 
-// fused-tail tiles (BM = OC) and plain tiles by M
-static TileCfg pick_tile(int M, bool fused) {
+// fused-tail tiles (BM = OC) and plain tiles by M (and N): 256 x 256 tiles
+// over 8 waves halve the L2 traffic per MFMA of the 128 x 128 tile, and are
+// used where they still give every CU a workgroup
+static TileCfg pick_tile(int M, bool fused, int64_t N = 0) {
     if (fused) {
         if (M == 128) return {128, 128, 2, 2};
         if (M == 64) return {64, 128, 1, 4};
         return {32, 256, 1, 4};
     }
+    if (M % 256 == 0 && (int64_t) (M / 256) * ((N + 255) / 256) >= 256) return {256, 256, 2, 4};
     if (M % 128 == 0) return {128, 128, 2, 2};
     if (M % 64 == 0) return {64, 256, 1, 4};
     return {32, 256, 1, 4};
@@ -358,8 +361,10 @@ static hipError_t launch_cfg(const ConvParams &p, int mode, int epi, int nsplit,
 template <typename TA, typename TO, typename TF, typename TT>
 static hipError_t launch_typed(ConvParams p, int mode, int epi, int nsplit, const TailArgs &ta,
                                hipStream_t st) {
-    const TileCfg tc = pick_tile(p.M, epi == EPI_TAIL);
+    const TileCfg tc = pick_tile(p.M, epi == EPI_TAIL, p.N);
     p.MT = p.M / tc.bm;
+    if (tc.bm == 256)
+        return launch_cfg<TA, TO, 256, 256, 2, 4, TF, TT>(p, mode, epi, nsplit, ta, st);
     if (tc.bm == 128 && tc.bn == 128)
         return launch_cfg<TA, TO, 128, 128, 2, 2, TF, TT>(p, mode, epi, nsplit, ta, st);
     if (tc.bm == 64 && tc.bn == 128)
