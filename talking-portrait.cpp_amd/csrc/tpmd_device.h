@@ -53,22 +53,27 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // upfirdn2d(up=2, pad=(2,1)) of one SP plane at output (X, Y), 4x4 kernel
-// k4[i + 4j] (patch :996-1018 semantics): the zero-stuffed window hits at
-// most 2x2 source pixels; accumulation order j-major, i-minor, skipping the
-// zero-stuffed taps exactly like the reference loop.
+// k4[i + 4j] (patch :996-1018 semantics).  Of the 4x4 window over the
+// zero-stuffed map, only taps with X+i-2 and Y+j-2 even hit a source pixel:
+// i in {X&1, X&1 + 2}, j in {Y&1, Y&1 + 2}, i.e. source columns
+// (X + (X&1) - 2)/2 + {0, 1} and the same for rows.  They are visited in
+// the reference loop's order (j-major, i-minor, out-of-map taps skipped), so
+// the sum equals the 16-tap loop's bit for bit.
 __device__ __forceinline__ float upfirdn2x_at(const float *__restrict__ plane, int W, int H,
                                               const float *__restrict__ k4, int X, int Y) {
 #pragma clang fp contract(off)
+    const int i0 = X & 1, j0 = Y & 1;
+    const int sx0 = (X + i0 - 2) >> 1, sy0 = (Y + j0 - 2) >> 1;
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int vy = Y + j - 2;
-        if (vy < 0 || vy >= 2 * H || (vy & 1)) continue;
+    for (int jj = 0; jj < 2; jj++) {
+        const int sy = sy0 + jj;
+        if (sy < 0 || sy >= H) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int vx = X + i - 2;
-            if (vx < 0 || vx >= 2 * W || (vx & 1)) continue;
-            acc += plane[(vx >> 1) + W * (vy >> 1)] * k4[i + 4 * j];
+        for (int ii = 0; ii < 2; ii++) {
+            const int sx = sx0 + ii;
+            if (sx < 0 || sx >= W) continue;
+            acc += plane[sx + W * sy] * k4[i0 + 2 * ii + 4 * (j0 + 2 * jj)];
         }
     }
     return acc;

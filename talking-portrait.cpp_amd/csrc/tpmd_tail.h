@@ -292,6 +292,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
             ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
             ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
         }
+        // taps and weights exactly as the reference selects them; the
+        // weighted sum as one fused multiply-add per channel and tap
         float smp[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) smp[e] = 0.0f;
@@ -300,7 +302,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
             if (!in[k]) continue;
             const float wk = tap_weight(t, k);
 #pragma unroll
-            for (int e = 0; e < 8; e++) smp[e] += wk * fv[k][e];
+            for (int e = 0; e < 8; e++) smp[e] = __builtin_fmaf(wk, fv[k][e], smp[e]);
         }
         float warp[8], trunk[8];
         const float one_m = 1.0f - m;
