@@ -43,12 +43,31 @@ template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ half_t from_f32<half_t>(float v) { return (half_t) v; }
 
+// v of the lane `lane ^ M` (M a power of two < 64): DPP quad permutes for
+// M = 1, 2 (no LDS traffic), ds_swizzle bit-masks for M = 4, 8, 16 (within
+// 32 lanes, no LDS addressing), ds_bpermute for M = 32
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    int y;
+    if constexpr (M == 1) y = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);       // [1,0,3,2]
+    else if constexpr (M == 2) y = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+    else if constexpr (M < 32) y = __builtin_amdgcn_ds_swizzle(x, 0x1F | (M << 10));
+    else y = __builtin_bit_cast(int, __shfl_xor(v, M, 64));
+    return __builtin_bit_cast(float, y);
+}
+
 // sum over aligned groups of G lanes (G a power of two <= 64), result in
-// every lane of the group: butterfly over DPP-able xor shuffles
+// every lane of the group: xor butterfly, each step adding the partner's
+// value to the lane's own (so every lane ends with the same bits)
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    if constexpr (G >= 2) v += lane_xor<1>(v);
+    if constexpr (G >= 4) v += lane_xor<2>(v);
+    if constexpr (G >= 8) v += lane_xor<4>(v);
+    if constexpr (G >= 16) v += lane_xor<8>(v);
+    if constexpr (G >= 32) v += lane_xor<16>(v);
+    if constexpr (G >= 64) v += lane_xor<32>(v);
     return v;
 }
 
