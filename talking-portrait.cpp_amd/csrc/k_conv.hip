@@ -420,7 +420,10 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     const int epi = fused ? EPI_TAIL : (nsplit > 1 ? EPI_PARTIAL : EPI_STORE);
     const TailArgs ta = fused ? *c.tail : TailArgs{};
     hipError_t e;
-    if (c.f16) {
+    const TileCfg tc = pick_tile(p.M, fused, p.N);
+    if (c.f16 && !fused && tc.bm == 256 && c.IC % 32 == 0) {
+        e = launch_modconv_async(p, c.mode, epi, nsplit, c.out_f16, st);
+    } else if (c.f16) {
         if (fused) {
             e = c.trunk_f16 ? launch_typed<half_t, float, half_t, half_t>(p, c.mode, epi, 1, ta, st)
                             : launch_typed<half_t, float, half_t, float>(p, c.mode, epi, 1, ta, st);
