@@ -153,6 +153,10 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, T
         });
     };
 
+    // the stage tail's skips do not depend on the conv: load them first
+    tail_skip sk;
+    if constexpr (EPI == EPI_TAIL) sk = tile_tail_skips<BN, 0>(ta, n0, tid);
+
     floatx16 acc[TM][TN];
 #pragma unroll
     for (int a = 0; a < TM; a++)
@@ -238,7 +242,10 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_kernel(ConvParams p, T
                 }
             }
         }
-        tile_tail<TF, TT, BM, BN, NT, 0>(ta, so, n0, tid);
+        tile_tail_wfs<BM, NT>(ta, so + tile_tail_lds<BM, BN>::WFS0, fr, tid);
+        __syncthreads();
+        tile_tail<TF, TT, BM, BN, NT, 0>(ta, so, so + tile_tail_lds<BM, BN>::PRM0,
+                                         so + tile_tail_lds<BM, BN>::WFS0, n0, tid, sk);
     }
 }
 
@@ -414,7 +421,7 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
                   (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
         return hipErrorInvalidValue;
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
-        return launch_modconv_halo(p, c.mode, c.out_f16, c.tail, c.trunk_f16, st);
+        return launch_modconv_halo(p, c.mode, c.out_f16, st);
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);
     if (nsplit > 1 && (!c.ws || c.ws_elems < (int64_t) nsplit * p.M * p.N)) nsplit = 1;
     const int epi = fused ? EPI_TAIL : (nsplit > 1 ? EPI_PARTIAL : EPI_STORE);

@@ -16,9 +16,10 @@
 //     the next tile's halo is loaded into registers while the current one is
 //     multiplied, so a tile costs one LDS commit and two barriers.
 //
-// Epilogues as k_conv.hip: EPI_STORE (dense or composed sub-pixel up-conv
-// store, 1/den + bias + leaky + next style) or EPI_TAIL (dense conv whose
-// activated tile goes to LDS for the two-phase stage tail, tpmd_tail.h).
+// Epilogue: the store epilogue of k_conv.hip (dense or composed sub-pixel
+// up-conv store, 1/den + bias + leaky + next style).  With the stage tail the
+// A fragments keep one workgroup per CU and the tail's gather latency is
+// exposed, so the fused conv + tail stages use the other kernels.
 //
 // MFMA: v_mfma_f32_32x32x16_f16; a 32-column block of the output is one row
 // of the tile (32 consecutive pixels), lane % 32 its column.
@@ -26,11 +27,11 @@
 
 namespace tpmd {
 
-template <int IC, int M, int EPI>
+template <int IC, int M>
 struct halo_cfg {
     static constexpr int NT = 256;
     static constexpr int WM = M / 32, WN = 4 / WM;       // waves along M / along tile rows
-    static constexpr int TH = (M == 128 || (IC == 64 && EPI == EPI_TAIL)) ? 4 : 8;
+    static constexpr int TH = M == 128 ? 4 : 8;
     static constexpr int TW = 32;
     static constexpr int TN = TH / WN;                  // tile rows per wave
     static constexpr int BN = TH * TW;                  // pixels per tile
@@ -42,15 +43,14 @@ struct halo_cfg {
     static constexpr int KS = IC / 16;                  // MFMA k steps per tap
     static constexpr int NAF = 9 * KS;                  // A fragments per wave
     static constexpr int HALO_BYTES = HPX * ROWB;
-    static constexpr int TAIL_BYTES = EPI == EPI_TAIL ? tile_tail_lds<M, BN>::FLOATS * 4 : 0;
-    static constexpr int LDS = HALO_BYTES > TAIL_BYTES ? HALO_BYTES : TAIL_BYTES;
+    static constexpr int LDS = HALO_BYTES;
     static_assert(WM * WN == 4 && TN * WN == TH, "wave layout");
 };
 
-template <int IC, int M, int MODE, int EPI, typename TO, typename TT>
-__global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArgs ta, int tiles_x,
+template <int IC, int M, int MODE, typename TO>
+__global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, int tiles_x,
                                                            int tiles_y, int ntiles) {
-    typedef halo_cfg<IC, M, EPI> C;
+    typedef halo_cfg<IC, M> C;
     typedef half_t TA;
     constexpr int NT = C::NT, TW = C::TW, TN = C::TN, HWD = C::HWD, ROWB = C::ROWB;
     constexpr int CPP = C::CPP, HCH = C::HCH, PF = C::PF, KS = C::KS, NAF = C::NAF;
@@ -141,39 +141,17 @@ __global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArg
         int b0, y0, x0;
         origin(t, b0, y0, x0);
         const int n0 = (b0 * H + y0) * W + x0;  // top-left pixel of the tile
-        if constexpr (EPI == EPI_STORE) {
 #pragma unroll
-            for (int b = 0; b < TN; b++) {
-                const int n = n0 + (wn * TN + b) * W + lrow;
+        for (int b = 0; b < TN; b++) {
+            const int n = n0 + (wn * TN + b) * W + lrow;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = wm * 32 + i * 8 + (lane >> 5) * 4;
-                    const float q[4] = {acc[b][i * 4], acc[b][i * 4 + 1], acc[b][i * 4 + 2], acc[b][i * 4 + 3]};
-                    epi_store_quad<TO, MODE>(p, q, m, n);
-                }
+            for (int i = 0; i < 4; i++) {
+                const int m = wm * 32 + i * 8 + (lane >> 5) * 4;
+                const float q[4] = {acc[b][i * 4], acc[b][i * 4 + 1], acc[b][i * 4 + 2], acc[b][i * 4 + 3]};
+                epi_store_quad<TO, MODE>(p, q, m, n);
             }
-            __syncthreads();  // halo reads done before the next commit
-        } else {
-            __syncthreads();  // halo reads done: the LDS becomes the tail's
-            constexpr int SOS = tile_tail_lds<M, C::BN>::SOS;
-            float *so = (float *) smem;
-#pragma unroll
-            for (int b = 0; b < TN; b++) {
-                const int col = (wn * TN + b) * TW + lrow;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int row = wm * 32 + i * 8 + (lane >> 5) * 4;
-                    const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) b0 * p.OC + row);
-                    const floatx4 bb = *(const floatx4 *) (p.bias + row);
-                    floatx4 v;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) v[j] = leaky(acc[b][i * 4 + j] * id[j] + bb[j]);
-                    *(floatx4 *) (so + col * SOS + row) = v;
-                }
-            }
-            tile_tail<TA, TT, M, C::BN, NT, TW>(ta, so, n0, tid);
-            __syncthreads();  // tail's LDS reads done before the next commit
         }
+        __syncthreads();  // halo reads done before the next commit
     }
 }
 
@@ -182,12 +160,9 @@ __global__ __launch_bounds__(256) void modconv_halo_kernel(ConvParams p, TailArg
 
 bool modconv_halo_ok(bool f16, int mode, int IC, int OC, int H, int W, bool tail) {
     const int M = mode == MODE_DENSE ? OC : 4 * OC;
-    if (!f16 || (IC != 32 && IC != 64) || (M != 32 && M != 64 && M != 128)) return false;
-    // with the stage tail the A fragments keep one workgroup per CU, and the
-    // tail's gather latency is then exposed: those stages use k_conv.hip
-    if (tail) return false;
+    if (!f16 || tail || (IC != 32 && IC != 64) || (M != 32 && M != 64 && M != 128)) return false;
     if (mode == MODE_SUBPIX && M != 128) return false;
-    const int th = (M == 128 || (IC == 64 && tail)) ? 4 : 8;  // halo_cfg::TH
+    const int th = M == 128 ? 4 : 8;  // halo_cfg::TH
     return W % 32 == 0 && H % th == 0;
 }
 
@@ -202,58 +177,45 @@ static int cu_count() {
     return n;
 }
 
-template <int IC, int M, int MODE, int EPI, typename TO, typename TT>
-static hipError_t launch_halo_k(const ConvParams &p, const TailArgs &ta, hipStream_t st) {
-    typedef halo_cfg<IC, M, EPI> C;
+template <int IC, int M, int MODE, typename TO>
+static hipError_t launch_halo_k(const ConvParams &p, hipStream_t st) {
+    typedef halo_cfg<IC, M> C;
     const int tiles_x = p.W / C::TW, tiles_y = p.H / C::TH;
     const int nframes = p.N / (p.H * p.W);
     const int ntiles = tiles_x * tiles_y * nframes;
-    auto kern = modconv_halo_kernel<IC, M, MODE, EPI, TO, TT>;
+    auto kern = modconv_halo_kernel<IC, M, MODE, TO>;
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, C::NT, 0) != hipSuccess || occ < 1) occ = 1;
     int grid = cu_count() * occ;
     if (grid > ntiles) grid = ntiles;
-    hipLaunchKernelGGL(kern, dim3((unsigned) grid), dim3(C::NT), 0, st, p, ta, tiles_x, tiles_y, ntiles);
+    hipLaunchKernelGGL(kern, dim3((unsigned) grid), dim3(C::NT), 0, st, p, tiles_x, tiles_y, ntiles);
     return hipGetLastError();
 }
 
-template <int IC, int M, typename TO, typename TT>
-static hipError_t launch_halo_m(const ConvParams &p, int mode, bool tail, const TailArgs &ta,
-                                hipStream_t st) {
-    if (tail) {
-        if constexpr (M <= 64) return launch_halo_k<IC, M, MODE_DENSE, EPI_TAIL, TO, TT>(p, ta, st);
-        return hipErrorInvalidValue;
-    }
-    if (mode == MODE_DENSE) return launch_halo_k<IC, M, MODE_DENSE, EPI_STORE, TO, TT>(p, ta, st);
-    if constexpr (M == 128) return launch_halo_k<IC, M, MODE_SUBPIX, EPI_STORE, TO, TT>(p, ta, st);
+template <int IC, int M, typename TO>
+static hipError_t launch_halo_m(const ConvParams &p, int mode, hipStream_t st) {
+    if (mode == MODE_DENSE) return launch_halo_k<IC, M, MODE_DENSE, TO>(p, st);
+    if constexpr (M == 128) return launch_halo_k<IC, M, MODE_SUBPIX, TO>(p, st);
     return hipErrorInvalidValue;
 }
 
-template <typename TO, typename TT>
-static hipError_t launch_halo_t(const ConvParams &p, int mode, bool tail, const TailArgs &ta,
-                                hipStream_t st) {
+template <typename TO>
+static hipError_t launch_halo_t(const ConvParams &p, int mode, hipStream_t st) {
     const int M = p.M;
     if (p.IC == 32) {
-        if (M == 32) return launch_halo_m<32, 32, TO, TT>(p, mode, tail, ta, st);
-        if (M == 64) return launch_halo_m<32, 64, TO, TT>(p, mode, tail, ta, st);
-        return launch_halo_m<32, 128, TO, TT>(p, mode, tail, ta, st);
+        if (M == 32) return launch_halo_m<32, 32, TO>(p, mode, st);
+        if (M == 64) return launch_halo_m<32, 64, TO>(p, mode, st);
+        return launch_halo_m<32, 128, TO>(p, mode, st);
     }
-    if (M == 32) return launch_halo_m<64, 32, TO, TT>(p, mode, tail, ta, st);
-    if (M == 64) return launch_halo_m<64, 64, TO, TT>(p, mode, tail, ta, st);
-    return launch_halo_m<64, 128, TO, TT>(p, mode, tail, ta, st);
+    if (M == 32) return launch_halo_m<64, 32, TO>(p, mode, st);
+    if (M == 64) return launch_halo_m<64, 64, TO>(p, mode, st);
+    return launch_halo_m<64, 128, TO>(p, mode, st);
 }
 
-// f16 operands; out_f16: stored activation type (EPI_STORE); tail: fused
-// stage tail with an f16 (trunk_f16) or f32 trunk
-hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, const TailArgs *tail,
-                               bool trunk_f16, hipStream_t st) {
-    if (tail) {
-        if (trunk_f16) return launch_halo_t<float, half_t>(p, mode, true, *tail, st);
-        return launch_halo_t<float, float>(p, mode, true, *tail, st);
-    }
-    const TailArgs none{};
-    if (out_f16) return launch_halo_t<half_t, half_t>(p, mode, false, none, st);
-    return launch_halo_t<float, half_t>(p, mode, false, none, st);
+// f16 operands; out_f16: stored activation type
+hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, hipStream_t st) {
+    if (out_f16) return launch_halo_t<half_t>(p, mode, st);
+    return launch_halo_t<float>(p, mode, st);
 }
 
 }  // namespace tpmd

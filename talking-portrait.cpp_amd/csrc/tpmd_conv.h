@@ -109,8 +109,7 @@ __device__ __forceinline__ void epi_store_quad(const ConvParams &p, const float 
 
 // k_conv_halo.hip: the A-stationary halo-tile kernel for IC in {32, 64}
 bool modconv_halo_ok(bool f16, int mode, int IC, int OC, int H, int W, bool tail);
-hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, const TailArgs *tail,
-                               bool trunk_f16, hipStream_t st);
+hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, hipStream_t st);
 
 // k_conv_async.hip: f16 store / split-K convs on 256 x 256 tiles (8 waves)
 // with LDS-DMA operand loads into a 4-stage ring; M % 256 == 0, IC % 32 == 0

@@ -178,10 +178,12 @@ namespace tpmd {
 // workgroup in two phases (same arithmetic as tail_pixel):
 //   phase 1, one thread per pixel: ToFlow dot (the style-folded weights
 //     Wf * s_f of the tile's frame are staged in LDS), flow skip, flow head,
-//     bilinear tap geometry, rgb skip; the per-pixel results go to LDS;
+//     bilinear tap geometry; the per-pixel results go to LDS;
 //   phase 2, G = C/8 lanes per pixel: gather of the feature taps, warp,
 //     trunk (* next style, stored), ToRGB with a butterfly over the G lanes.
-// Per-pixel scalar work runs once instead of on each of the G lanes.
+// Per-pixel scalar work runs once instead of on each of the G lanes.  The
+// flow / rgb skips do not depend on the conv output: tile_tail_skips loads
+// them before the conv runs, so their latency hides behind it.
 template <int C, int BN>
 struct tile_tail_lds {
     static constexpr int SOS = C + 4;                 // out row stride (floats)
@@ -196,32 +198,84 @@ struct tile_tail_lds {
 // consecutive pixels starting at batch pixel n0) or pix0 + (p / TWC) * r +
 // p % TWC (TWC > 0: a TWC-wide block of rows whose top-left pixel is n0).  Every
 // pixel of the tile exists (the caller's tiling guarantees it).
+template <int TWC>
+__device__ __forceinline__ int tile_pix(int pix0, int r, int p) {
+    if constexpr (TWC > 0) return pix0 + (p / TWC) * r + p % TWC;
+    return pix0 + p;
+}
+
+// upfirdn2x skips of the flow and rgb heads for tile pixel tid (tid < BN)
+struct tail_skip {
+    float fl[3], rgb[3];
+};
+
+template <int BN, int TWC>
+__device__ __forceinline__ tail_skip tile_tail_skips(const TailArgs &a, int n0, int tid) {
+#pragma clang fp contract(off)
+    tail_skip sk;
+#pragma unroll
+    for (int k = 0; k < 3; k++) sk.fl[k] = sk.rgb[k] = 0.0f;
+    if (tid < BN && (a.flow_prev || a.rgb_prev)) {
+        const int r = a.r, rh = r >> 1, RR = r * r;
+        const int fr = n0 / RR;
+        const int pix = tile_pix<TWC>(n0 - fr * RR, r, tid);
+        const int y = pix / r, x = pix - y * r;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            if (a.flow_prev)
+                sk.fl[k] = upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
+            if (a.rgb_prev)
+                sk.rgb[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+        }
+    }
+    return sk;
+}
+
+// folded ToFlow weights of frame fr (gemm_weight: W * s rounded to f32)
+template <int C, int NT>
+__device__ __forceinline__ void tile_tail_wfs(const TailArgs &a, float *wfs, int fr, int tid) {
+    for (int i = tid; i < 3 * C; i += NT) {
+        const int c = i % C;
+        wfs[i] = a.wflow[i] * a.sflow[(int64_t) fr * C + c];
+    }
+}
+
+// 8 channels of one feature tap, kept in the stored type until used
+template <typename T> struct feat8;
+template <> struct feat8<half_t> {
+    half8 h;
+    __device__ __forceinline__ void load(const half_t *p) { h = *(const half8 *) p; }
+    __device__ __forceinline__ float operator[](int e) const { return (float) h[e]; }
+};
+template <> struct feat8<float> {
+    floatx4 lo, hi;
+    __device__ __forceinline__ void load(const float *p) {
+        lo = *(const floatx4 *) p;
+        hi = *(const floatx4 *) (p + 4);
+    }
+    __device__ __forceinline__ float operator[](int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
+};
+
+// Runs after the activated tile `so` ([BN][SOS] f32) and `wfs` are written
+// and a barrier has made them visible; prm is [BN][PRM] scratch.
 template <typename TF, typename TT, int C, int BN, int NT, int TWC>
-__device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0, int tid) {
+__device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, float *prm, const float *wfs,
+                                          int n0, int tid, const tail_skip &sk) {
 #pragma clang fp contract(off)
     typedef tile_tail_lds<C, BN> L;
     constexpr int G = C / 8;
     constexpr int PPW = 64 / G;
     constexpr int PPB = (NT / 64) * PPW;
     static_assert(BN % PPB == 0, "tail pass");
-    const int r = a.r, rh = r >> 1;
+    const int r = a.r;
     const int RR = r * r;
     const int fr = n0 / RR;                          // the tile lies in one frame
     const int pix0 = n0 - fr * RR;
-    auto pix_of = [&](int p) { return TWC ? pix0 + (p / (TWC ? TWC : 1)) * r + p % (TWC ? TWC : 1) : pix0 + p; };
-    float *so = lds, *prm = lds + L::PRM0, *wfs = lds + L::WFS0;
-
-    // folded ToFlow weights of this frame (gemm_weight: W * s rounded to f32)
-    for (int i = tid; i < 3 * C; i += NT) {
-        const int c = i % C;
-        wfs[i] = a.wflow[i] * a.sflow[(int64_t) fr * C + c];
-    }
-    __syncthreads();
 
     // ---- phase 1: one thread per pixel
     if (tid < BN) {
         const int p = tid;
-        const int pix = pix_of(p);
+        const int pix = tile_pix<TWC>(pix0, r, p);
         const int y = pix / r, x = pix - y * r;
         float fl[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -235,13 +289,10 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
                 fl[k] = __builtin_fmaf(wfs[k * C + c + 3], o[3], fl[k]);
             }
         }
-        float up[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             fl[k] = fl[k] + a.fbias[k];
-            if (a.flow_prev)
-                fl[k] = fl[k] + upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
-            if (a.rgb_prev) up[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+            if (a.flow_prev) fl[k] = fl[k] + sk.fl[k];
         }
         if (a.flow_cur) {
 #pragma unroll
@@ -252,11 +303,16 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
         const float m = 1.0f / (1.0f + expf(-fl[2]));
         const taps4 t = gather_geometry(gx, gy, r, r);
         *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
-        *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, up[0], up[1], up[2]};
+        *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
     }
     __syncthreads();
 
-    // ---- phase 2: G lanes per pixel, 8 channels each
+    // ---- phase 2: G lanes per pixel, 8 channels each; the feature taps of
+    // NB pixels are requested together, then used
+    constexpr int ITER = BN / PPB;
+    constexpr int NBMAX = sizeof(TF) == 2 ? 4 : 2;
+    constexpr int NB = ITER < NBMAX ? ITER : NBMAX;
+    static_assert(ITER % NB == 0, "tail batch");
     const int lane = tid & 63, wid = tid >> 6;
     const int gl = lane % G, grp = lane / G;
     const int c0 = gl * 8;
@@ -265,75 +321,82 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, float *lds, int n0,
     for (int k = 0; k < 3; k++) load8<float>::run(a.wrgb + k * C + c0, wr[k]);
     if (a.s_next) load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
     const TF *feat = (const TF *) a.feat;
-    for (int lp0 = 0; lp0 < BN; lp0 += PPB) {
-        const int lp = lp0 + wid * PPW + grp;
-        const int pix = pix_of(lp);
-        const int64_t pp = (int64_t) fr * RR + pix;
-        const floatx4 q0 = *(const floatx4 *) (prm + lp * L::PRM);
-        const floatx4 q1 = *(const floatx4 *) (prm + lp * L::PRM + 4);
-        taps4 t;
-        t.x0 = __float_as_int(q0[0]);
-        t.y0 = __float_as_int(q0[1]);
-        t.wx = q0[2];
-        t.wy = q0[3];
-        const float m = q1[0];
-        float fv[4][8];
-        bool in[4];
+    for (int it0 = 0; it0 < ITER; it0 += NB) {
+        taps4 t[NB];
+        float m[NB];
+        bool in[NB][4];
+        feat8<TF> fv[NB][4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
-            in[k] = cx >= 0 && cx < r && cy >= 0 && cy < r;
-            if (in[k]) load8<TF>::run(feat + (int64_t) (cy * r + cx) * C + c0, fv[k]);
-        }
-        float ov[8];
-        {
-            const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
-            const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
-            ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
-            ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
-        }
-        // taps and weights exactly as the reference selects them; the
-        // weighted sum as one fused multiply-add per channel and tap
-        float smp[8];
+        for (int b = 0; b < NB; b++) {
+            const int lp = (it0 + b) * PPB + wid * PPW + grp;
+            const floatx4 q0 = *(const floatx4 *) (prm + lp * L::PRM);
+            t[b].x0 = __float_as_int(q0[0]);
+            t[b].y0 = __float_as_int(q0[1]);
+            t[b].wx = q0[2];
+            t[b].wy = q0[3];
+            m[b] = prm[lp * L::PRM + 4];
 #pragma unroll
-        for (int e = 0; e < 8; e++) smp[e] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (!in[k]) continue;
-            const float wk = tap_weight(t, k);
-#pragma unroll
-            for (int e = 0; e < 8; e++) smp[e] = __builtin_fmaf(wk, fv[k][e], smp[e]);
-        }
-        float warp[8], trunk[8];
-        const float one_m = 1.0f - m;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            warp[e] = smp[e] * m;
-            trunk[e] = warp[e] + ov[e] * one_m;
-        }
-        if (a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
-        if (a.trunk) {
-            if (a.s_next) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
+            for (int k = 0; k < 4; k++) {
+                const int cx = t[b].x0 + (k & 1), cy = t[b].y0 + (k >> 1);
+                in[b][k] = cx >= 0 && cx < r && cy >= 0 && cy < r;
+                if (in[b][k]) fv[b][k].load(feat + (int64_t) (cy * r + cx) * C + c0);
             }
-            store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
         }
-        float rgb[3];
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            float acc = 0.0f;
+        for (int b = 0; b < NB; b++) {
+            const int lp = (it0 + b) * PPB + wid * PPW + grp;
+            const int pix = tile_pix<TWC>(pix0, r, lp);
+            const int64_t pp = (int64_t) fr * RR + pix;
+            float ov[8];
+            {
+                const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
+                const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
+                ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
+                ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
+            }
+            // taps and weights exactly as the reference selects them; the
+            // weighted sum as one fused multiply-add per channel and tap
+            float smp[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc = __builtin_fmaf(wr[k][e], warp[e], acc);
-            rgb[k] = group_sum<G>(acc);
-        }
-        if (gl < 3) {
-            const int k = gl;
-            const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
-            float v = leaky(rv + a.rlb[k]);
-            v = v + a.rbias[k];
-            if (a.rgb_prev) v = v + (k == 0 ? q1[1] : (k == 1 ? q1[2] : q1[3]));
-            a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
+            for (int e = 0; e < 8; e++) smp[e] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (!in[b][k]) continue;
+                const float wk = tap_weight(t[b], k);
+#pragma unroll
+                for (int e = 0; e < 8; e++) smp[e] = __builtin_fmaf(wk, fv[b][k][e], smp[e]);
+            }
+            float warp[8], trunk[8];
+            const float one_m = 1.0f - m[b];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                warp[e] = smp[e] * m[b];
+                trunk[e] = warp[e] + ov[e] * one_m;
+            }
+            if (a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
+            if (a.trunk) {
+                if (a.s_next) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
+                }
+                store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
+            }
+            float rgb[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc = __builtin_fmaf(wr[k][e], warp[e], acc);
+                rgb[k] = group_sum<G>(acc);
+            }
+            if (gl < 3) {
+                const int k = gl;
+                const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
+                float v = leaky(rv + a.rlb[k]);
+                v = v + a.rbias[k];
+                if (a.rgb_prev) v = v + prm[lp * L::PRM + 5 + k];
+                a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
+            }
         }
     }
 }
