@@ -422,6 +422,10 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
         return hipErrorInvalidValue;
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
+    if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H))
+        return launch_modconv_fused32(p, *c.tail, c.trunk_f16, st);
+    if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H))
+        return launch_modconv_tail_async(p, *c.tail, c.trunk_f16, st);
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);
     if (nsplit > 1 && (!c.ws || c.ws_elems < (int64_t) nsplit * p.M * p.N)) nsplit = 1;
     const int epi = fused ? EPI_TAIL : (nsplit > 1 ? EPI_PARTIAL : EPI_STORE);

@@ -207,6 +207,175 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_async_kernel(ConvParam
 }
 
 // ---------------------------------------------------------------------------
+// Dense conv + stage tail (OC = BM in {32, 64, 128}, one frame per tile of BN
+// pixels): the same DMA ring and fragment pipeline, then the activated tile
+// goes to LDS and the two-phase stage tail of tpmd_tail.h runs on it.  The
+// (BM + BN) / 16 row groups of a k tile are dealt to the waves round robin;
+// a wave that moves fewer groups than another waits on the smaller count,
+// which only waits longer.  The tail's skips and the frame's folded ToFlow
+// weights are fetched before the k loop.
+template <int C, int BN, int S>
+struct tail_async_cfg {
+    static constexpr int RB = 64;
+    static constexpr int STAGE = (C + BN) * RB;
+    static constexpr int RING = S * STAGE;
+    typedef tile_tail_lds<C, BN> L;
+    static constexpr int TAIL = L::WFS0 * 4;                   // so + prm, over the ring
+    static constexpr int WFS = RING > TAIL ? RING : TAIL;       // byte offset of wfs
+    static constexpr int LDS = WFS + 3 * C * 4;
+};
+
+template <typename TF, typename TT, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(ConvParams p, TailArgs ta) {
+    typedef half_t TA;
+    typedef tail_async_cfg<BM, BN, S> C;
+    typedef typename C::L L;
+    constexpr int NT = WM * WN * 64, NW = WM * WN;
+    constexpr int RB = C::RB, BK = RB / 2, KS = RB / 32;
+    constexpr int NG = (BM + BN) / 16;                 // 16-row DMA groups per k tile
+    constexpr int SLOTS = (NG + NW - 1) / NW, LPW = NG / NW;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+    static_assert(BM % 16 == 0 && BN % 16 == 0 && LPW >= 1, "row groups");
+    static_assert(TM >= 1 && TN >= 1, "wave tile");
+    static_assert(S >= 3 && KS == 2, "pipeline");
+
+    __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+    float *so = (float *) smem, *prm = so + L::PRM0, *wfs = (float *) (smem + C::WFS);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid / WN, wn = wid % WN;
+    const int n0 = xcd_remap((int) blockIdx.x, (int) gridDim.x) * BN;
+    const int IC = p.IC, H = p.H, W = p.W;
+    const int K = 9 * IC;
+    const int HW = H * W;
+    const int kpt = IC / BK;
+    const int fr = n0 / HW;
+    const int T = p.T;
+
+    // conv-independent tail inputs first
+    const tail_skip sk = tile_tail_skips<BN, 0>(ta, n0, tid);
+    tile_tail_wfs<BM, NT>(ta, wfs, fr, tid);
+
+    // DMA slots: slot j of wave w moves row group g = j * NW + w
+    const int lrow16 = lane >> 2, lpos = lane & 3;
+    const TA *Ap = (const TA *) p.A, *Xp = (const TA *) p.X;
+    const TA *src[SLOTS];
+    unsigned smask[SLOTS];  // taps whose source lies in the map (all for A rows)
+#pragma unroll
+    for (int j = 0; j < SLOTS; j++) {
+        const int row = (j * NW + wid) * 16 + lrow16;
+        const int chunk = (lpos ^ swz(row)) * 8;
+        src[j] = Xp;
+        smask[j] = 0;
+        if (row < BM) {
+            src[j] = Ap + (int64_t) row * K + chunk;
+            smask[j] = 0x1FFu;
+        } else if (row < BM + BN) {
+            const int rem = n0 - fr * HW + row - BM;
+            const int y = rem / W, x = rem - y * W;
+            src[j] = Xp + (int64_t) fr * p.x_bstride + (int64_t) rem * IC + chunk;
+#pragma unroll
+            for (int tap = 0; tap < 9; tap++) {
+                const int iy = y + tap / 3 - 1, ix = x + tap % 3 - 1;
+                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W) smask[j] |= 1u << tap;
+            }
+        }
+    }
+    const void *zero = (const void *) g_zero16;
+
+    int q_t = 0, q_tap = 0, q_ic0 = 0;  // next k tile to issue
+    auto issue = [&]() {
+        const int dy = q_tap / 3 - 1, dx = q_tap - (q_tap / 3) * 3 - 1;
+        const int boff = (dy * W + dx) * IC + q_ic0;
+        char *stage = smem + (q_t % S) * C::STAGE;
+        static_for<SLOTS>([&](auto j) {
+            const int g = j * NW + wid;
+            if (g < NG) {
+                const int off = g < BM / 16 ? q_t * BK : boff;
+                const void *gp = (smask[j] >> q_tap) & 1u ? (const void *) (src[j] + off) : zero;
+                __builtin_amdgcn_global_load_lds(gp, TPMD_LDS(stage + g * 16 * RB), 16, 0, 0);
+            }
+        });
+        q_t++;
+        q_ic0 += BK;
+        if (q_ic0 == IC) {
+            q_ic0 = 0;
+            q_tap++;
+        }
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; a++)
+#pragma unroll
+        for (int b = 0; b < TN; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+
+    const int lrow = lane & 31;
+    const int khalf = lane >> 5;
+    auto read_frags = [&](const char *st, int ks, u32x4 (&af)[TM], u32x4 (&bf)[TN]) {
+        const int kc = ks * 2 + khalf;
+        static_for<TM>([&](auto a) {
+            const int row = wm * WTM + a * 32 + lrow;
+            af[a] = *(const u32x4 *) (st + row * RB + ((kc ^ swz(row)) << 4));
+        });
+        static_for<TN>([&](auto b) {
+            const int row = BM + wn * WTN + b * 32 + lrow;
+            bf[b] = *(const u32x4 *) (st + row * RB + ((kc ^ swz(row)) << 4));
+        });
+    };
+    auto mfmas = [&](const u32x4 (&af)[TM], const u32x4 (&bf)[TN]) {
+        static_for<TM>([&](auto a) { static_for<TN>([&](auto b) { mfma_op<TA>::run(af[a], bf[b], acc[a][b]); }); });
+    };
+    auto stage_of = [&](int t) { return smem + (t % S) * C::STAGE; };
+
+#pragma unroll
+    for (int s = 0; s < S - 1; s++)
+        if (s < T) issue();
+    if (S - 2 < T) __builtin_amdgcn_s_waitcnt(waitcnt_vm((S - 2) * LPW));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    u32x4 a0[TM], b0[TN], a1[TM], b1[TN];
+    read_frags(stage_of(0), 0, a0, b0);
+    for (int t = 0; t < T; t++) {
+        read_frags(stage_of(t), 1, a1, b1);
+        mfmas(a0, b0);
+        if (t + 1 < T) {
+            if (t + S - 2 < T) __builtin_amdgcn_s_waitcnt(waitcnt_vm((S - 3) * LPW));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (t + S - 1 < T) issue();
+            read_frags(stage_of(t + 1), 0, a0, b0);
+        }
+        mfmas(a1, b1);
+    }
+    __syncthreads();  // every wave is done with the ring: it becomes the activated tile
+
+    // accumulator (a, b, v): channel a*32 + (v/4)*8 + (lane/32)*4 + v%4, pixel b*32 + lane%32
+    static_for<TN>([&](auto b) {
+        const int col = wn * WTN + b * 32 + lrow;
+        static_for<TM>([&](auto a) {
+            static_for<4>([&](auto i) {
+                const int row = wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
+                const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + row);
+                const floatx4 bb = *(const floatx4 *) (p.bias + row);
+                floatx4 v;
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                *(floatx4 *) (so + col * L::SOS + row) = v;
+            });
+        });
+    });
+    __syncthreads();
+    tile_tail<TF, TT, BM, BN, NT, 0>(ta, so, prm, wfs, n0, tid, sk);
+}
+
+// ---------------------------------------------------------------------------
 // host side: p.MT, p.T are set here
 
 template <typename TO, int BM, int BN, int WM, int WN, int S>
@@ -234,6 +403,42 @@ hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nspl
     if (p.M % 256 != 0 || p.IC % 32 != 0) return hipErrorInvalidValue;
     if (out_f16) return launch_async_cfg<half_t, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
     return launch_async_cfg<float, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
+}
+
+template <typename TT, int BM, int BN, int WM, int WN>
+static hipError_t launch_tail_cfg(ConvParams p, const TailArgs &ta, hipStream_t st) {
+    constexpr int S = 4;
+    p.MT = 1;
+    p.T = 9 * p.IC * 2 / tail_async_cfg<BM, BN, S>::RB;
+    if (p.M != BM || p.N % BN != 0 || (p.H * p.W) % BN != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((modconv3x3_tail_async_kernel<half_t, TT, BM, BN, WM, WN, S>), dim3((unsigned) (p.N / BN)),
+                       dim3(WM * WN * 64), 0, st, p, ta);
+    return hipGetLastError();
+}
+
+// measured: the ring pays at OC = 64; at OC = 128 the register-staged
+// k_conv.hip kernel (three workgroups per CU) is faster
+bool modconv_tail_async_ok(int OC, int r) {
+    if (OC == 32) return (r * r) % 256 == 0;
+    if (OC == 64) return (r * r) % 128 == 0;
+    return false;
+}
+
+hipError_t launch_modconv_tail_async(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
+    if (p.IC % 32 != 0) return hipErrorInvalidValue;
+    if (p.M == 32) {
+        if (trunk_f16) return launch_tail_cfg<half_t, 32, 256, 1, 4>(p, ta, st);
+        return launch_tail_cfg<float, 32, 256, 1, 4>(p, ta, st);
+    }
+    if (p.M == 64) {
+        if (trunk_f16) return launch_tail_cfg<half_t, 64, 128, 1, 4>(p, ta, st);
+        return launch_tail_cfg<float, 64, 128, 1, 4>(p, ta, st);
+    }
+    if (p.M == 128) {
+        if (trunk_f16) return launch_tail_cfg<half_t, 128, 128, 2, 2>(p, ta, st);
+        return launch_tail_cfg<float, 128, 128, 2, 2>(p, ta, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace tpmd

@@ -1,0 +1,148 @@
+// Dense 3x3 modulated conv + stage tail for the 32-channel stage
+// (IC = OC = 32, f16 operands; src/motion_dec.cpp:357-373 then :1077-1108):
+// the implicit GEMM of k_conv.hip on a halo tile, so every input pixel is
+// fetched once per tile instead of once per tap:
+//
+//   * a workgroup owns a TH x 32 block of output pixels of one frame; the
+//     (TH+2) x 34 input pixels around it (zero outside the map) are loaded
+//     into registers with the 32 x 288 weight matrix's MFMA A fragments
+//     (18 per lane, kept for the whole conv), then the halo goes to LDS with
+//     a 16-byte pad per pixel (conflict-free 32-pixel fragment reads);
+//   * wave w computes rows w*TH/4 .. of the block: for each tap (dy, dx) and
+//     16-channel step, the B fragment is the halo row shifted by (dy, dx);
+//   * the activated tile goes to LDS over the halo and the two-phase stage
+//     tail of tpmd_tail.h runs on it (the tail's skips and the folded ToFlow
+//     weights are fetched before the conv).
+// One global round trip for the conv instead of one per tap.
+#include "tpmd_conv.h"
+
+namespace tpmd {
+
+template <int TH>
+struct fused32_cfg {
+    static constexpr int C = 32, NT = 256, TW = 32, BN = TH * TW;
+    static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
+    static constexpr int PXB = C * 2 + 16;              // padded halo pixel (bytes)
+    static constexpr int CPP = C * 2 / 16;              // 16-byte chunks per pixel
+    static constexpr int HCH = HPX * CPP;
+    static constexpr int PF = (HCH + NT - 1) / NT;      // halo chunks per thread
+    static constexpr int KS = C / 16;                   // MFMA k steps per tap
+    static constexpr int NAF = 9 * KS;                  // A fragments
+    static constexpr int RPW = TH / 4;                  // output rows per wave
+    typedef tile_tail_lds<C, BN> L;
+    static constexpr int HALO = HPX * PXB;
+    static constexpr int TAIL = L::WFS0 * 4;            // so + prm
+    static constexpr int WFS = HALO > TAIL ? HALO : TAIL;
+    static constexpr int LDS = WFS + 3 * C * 4;
+    static_assert(TH % 4 == 0, "rows per wave");
+};
+
+template <typename TF, typename TT, int TH>
+__global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
+                                                          int tiles_frame) {
+    typedef half_t TA;
+    typedef fused32_cfg<TH> F;
+    typedef typename F::L L;
+    constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
+    constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, NAF = F::NAF, RPW = F::RPW;
+    constexpr int K = 9 * C;
+    __shared__ __attribute__((aligned(16))) char smem[F::LDS];
+    float *so = (float *) smem, *prm = so + L::PRM0, *wfs = (float *) (smem + F::WFS);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
+    const int fr = tile / tiles_frame;
+    const int trem = tile - fr * tiles_frame;
+    const int ty = trem / tiles_x, tx = trem - ty * tiles_x;
+    const int H = p.H, W = p.W;
+    const int y0 = ty * TH, x0 = tx * TW;
+    const int n0 = (fr * H + y0) * W + x0;  // top-left pixel of the block
+
+    // conv-independent tail inputs
+    const tail_skip sk = tile_tail_skips<BN, TW>(ta, n0, tid);
+    tile_tail_wfs<C, NT>(ta, wfs, fr, tid);
+
+    // halo and A fragments -> registers (one round trip)
+    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
+    u32x4 hv[PF];
+    static_for<PF>([&](auto i) {
+        const int ch = tid + i * NT;
+        hv[i] = u32x4{0u, 0u, 0u, 0u};
+        if (ch < HCH) {
+            const int px = ch / CPP, c = ch - px * CPP;
+            const int hy = px / HWD, hx = px - hy * HWD;
+            const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
+            if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
+                hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
+        }
+    });
+    const int lrow = lane & 31, khalf = lane >> 5;
+    u32x4 af[NAF];
+    {
+        const TA *arow = (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
+        static_for<NAF>([&](auto j) { af[j] = *(const u32x4 *) (arow + j * 16); });
+    }
+    static_for<PF>([&](auto i) {
+        const int ch = tid + i * NT;
+        if (ch < HCH) {
+            const int px = ch / CPP, c = ch - px * CPP;
+            *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
+        }
+    });
+    __syncthreads();
+
+    // conv: acc[b] = 32 channels x the 32 pixels of output row wid*RPW + b
+    floatx16 acc[RPW];
+    static_for<RPW>([&](auto b) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[b][v] = 0.0f;
+    });
+    static_for<9>([&](auto tap) {
+        constexpr int dy = tap / 3, dx = tap % 3;  // halo offsets of the tap
+        static_for<KS>([&](auto ks) {
+            static_for<RPW>([&](auto b) {
+                const int hrow = wid * RPW + b + dy;
+                const u32x4 bf =
+                    *(const u32x4 *) (smem + (hrow * HWD + lrow + dx) * PXB + (ks * 2 + khalf) * 16);
+                mfma_op<TA>::run(af[tap * KS + ks], bf, acc[b]);
+            });
+        });
+    });
+    __syncthreads();  // halo reads done: the LDS becomes the activated tile
+
+    // accumulator (b, v): channel (v/4)*8 + (lane/32)*4 + v%4, tile pixel (wid*RPW + b)*32 + lane%32
+    static_for<RPW>([&](auto b) {
+        const int col = (wid * RPW + b) * TW + lrow;
+        static_for<4>([&](auto i) {
+            const int row = i * 8 + khalf * 4;
+            const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * C + row);
+            const floatx4 bb = *(const floatx4 *) (p.bias + row);
+            floatx4 v;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = leaky(acc[b][i * 4 + j] * id[j] + bb[j]);
+            *(floatx4 *) (so + col * L::SOS + row) = v;
+        });
+    });
+    __syncthreads();
+    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
+}
+
+bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 32 && OC == 32 && r % 32 == 0; }
+
+hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
+    constexpr int TH = 8;
+    if (p.IC != 32 || p.OC != 32 || p.M != 32 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
+    const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
+    const int nframes = p.N / (p.H * p.W);
+    const dim3 grid((unsigned) (nframes * tiles_frame));
+    if (trunk_f16)
+        hipLaunchKernelGGL((conv32_tail_kernel<half_t, half_t, TH>), grid, dim3(256), 0, st, p, ta, tiles_x,
+                           tiles_frame);
+    else
+        hipLaunchKernelGGL((conv32_tail_kernel<half_t, float, TH>), grid, dim3(256), 0, st, p, ta, tiles_x,
+                           tiles_frame);
+    return hipGetLastError();
+}
+
+}  // namespace tpmd

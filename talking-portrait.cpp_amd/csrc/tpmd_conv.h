@@ -115,5 +115,13 @@ hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, hipS
 // with LDS-DMA operand loads into a 4-stage ring; M % 256 == 0, IC % 32 == 0
 hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16,
                                 hipStream_t st);
+// k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128}
+// (tiles of 256, 128, 128 pixels of one frame) with the same operand ring
+bool modconv_tail_async_ok(int OC, int r);
+// k_conv_fused.hip: f16 dense conv + fused stage tail for IC = OC = 32 on
+// halo tiles of 8 x 32 pixels (r % 32 == 0)
+bool modconv_fused32_ok(bool f16, int IC, int OC, int r);
+hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
+hipError_t launch_modconv_tail_async(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
 
 }  // namespace tpmd
