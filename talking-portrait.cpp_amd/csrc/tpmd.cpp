@@ -641,10 +641,10 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
         return -1;
     for (int j = 0; j < ns; j++) {
         const size_t r = (size_t) 8 << j;
-        c->st[j].feat = A(r * r * c->oc[j] * c->act_size());
+        const size_t fb = r * r * c->oc[j] * c->act_size() + TAIL_FEAT_PAD;  // + zero pad
+        c->st[j].feat = A(fb);
         if (!c->st[j].feat) return -1;
-        if (!c->hip_ok(hipMemset(c->st[j].feat, 0, r * r * c->oc[j] * c->act_size()), "memset"))
-            return -1;
+        if (!c->hip_ok(hipMemset(c->st[j].feat, 0, fb), "memset")) return -1;
     }
     c->built = true;
     return 0;

@@ -23,7 +23,9 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr float kSlope = 0.2f;
 
-__device__ __forceinline__ float leaky(float v) { return v > 0.0f ? v : kSlope * v; }
+// v > 0 ? v : 0.2 v, as one max: for v > 0, v > 0.2 v; otherwise 0.2 v >= v
+// (and both zeros and infinities come out as the select gives them)
+__device__ __forceinline__ float leaky(float v) { return __builtin_fmaxf(v, kSlope * v); }
 
 // 16-byte vector of act_t and its element count
 template <typename T> struct vec16;

@@ -26,9 +26,13 @@ struct DemodTable {
     int64_t d0[kMaxSeg];      // element offset of its 1/den block [frame][OC]
 };
 
+// zero bytes that follow every warp feature map: the fused stage tail reads
+// them for the bilinear taps outside the map
+constexpr int TAIL_FEAT_PAD = 64;
+
 struct TailArgs {
     const void *out;          // CL [frame][r*r][C] dense-conv output (TOUT)
-    const void *feat;         // [r*r][C] warp features (TF)
+    const void *feat;         // [r*r][C] warp features (TF), then TAIL_FEAT_PAD zero bytes
     const float *wflow;       // [3][C] ToFlow weight (scale-folded)
     const float *sflow;       // [frame][C] ToFlow style
     const float *fbias;       // [3]

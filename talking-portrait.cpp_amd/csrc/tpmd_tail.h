@@ -320,11 +320,17 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
 #pragma unroll
     for (int k = 0; k < 3; k++) load8<float>::run(a.wrgb + k * C + c0, wr[k]);
     if (a.s_next) load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
-    const TF *feat = (const TF *) a.feat;
+    // 32-bit byte offsets from per-frame bases; a tap outside the map reads
+    // the zero pad that follows the feature map (TAIL_FEAT_PAD bytes), whose
+    // product w * 0 = +0 leaves the running sum unchanged, as skipping it does
+    const char *featb = (const char *) a.feat;
+    const unsigned pad_off = (unsigned) RR * C * (unsigned) sizeof(TF);
+    char *trunkb = a.trunk ? (char *) a.trunk + (int64_t) fr * RR * C * (int64_t) sizeof(TT) : nullptr;
+    float *warpf = a.warp_tap ? a.warp_tap + (int64_t) fr * RR * C : nullptr;
+    float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
     for (int it0 = 0; it0 < ITER; it0 += NB) {
         taps4 t[NB];
         float m[NB];
-        bool in[NB][4];
         feat8<TF> fv[NB][4];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
@@ -335,18 +341,19 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
             t[b].wx = q0[2];
             t[b].wy = q0[3];
             m[b] = prm[lp * L::PRM + 4];
+            const bool inx[2] = {(unsigned) t[b].x0 < (unsigned) r, (unsigned) (t[b].x0 + 1) < (unsigned) r};
+            const bool iny[2] = {(unsigned) t[b].y0 < (unsigned) r, (unsigned) (t[b].y0 + 1) < (unsigned) r};
+            const unsigned base = ((unsigned) (t[b].y0 * r + t[b].x0) * C + c0) * (unsigned) sizeof(TF);
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int cx = t[b].x0 + (k & 1), cy = t[b].y0 + (k >> 1);
-                in[b][k] = cx >= 0 && cx < r && cy >= 0 && cy < r;
-                if (in[b][k]) fv[b][k].load(feat + (int64_t) (cy * r + cx) * C + c0);
+                const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * C * (int) sizeof(TF));
+                fv[b][k].load((const TF *) (featb + (inx[k & 1] && iny[k >> 1] ? off : pad_off)));
             }
         }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int lp = (it0 + b) * PPB + wid * PPW + grp;
             const int pix = tile_pix<TWC>(pix0, r, lp);
-            const int64_t pp = (int64_t) fr * RR + pix;
             float ov[8];
             {
                 const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
@@ -361,7 +368,6 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
             for (int e = 0; e < 8; e++) smp[e] = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                if (!in[b][k]) continue;
                 const float wk = tap_weight(t[b], k);
 #pragma unroll
                 for (int e = 0; e < 8; e++) smp[e] = __builtin_fmaf(wk, fv[b][k][e], smp[e]);
@@ -373,13 +379,14 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
                 warp[e] = smp[e] * m[b];
                 trunk[e] = warp[e] + ov[e] * one_m;
             }
-            if (a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
-            if (a.trunk) {
+            const unsigned po = (unsigned) pix * C + c0;
+            if (warpf) store8<float>(warpf + po, warp);
+            if (trunkb) {
                 if (a.s_next) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
                 }
-                store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
+                store8<TT>((TT *) (trunkb + po * (unsigned) sizeof(TT)), trunk);
             }
             float rgb[3];
 #pragma unroll
@@ -395,7 +402,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
                 float v = leaky(rv + a.rlb[k]);
                 v = v + a.rbias[k];
                 if (a.rgb_prev) v = v + prm[lp * L::PRM + 5 + k];
-                a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
+                rgbf[(unsigned) (k * RR + pix)] = v;
             }
         }
     }
