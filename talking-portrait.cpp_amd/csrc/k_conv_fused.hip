@@ -12,7 +12,8 @@
 //     16-channel step, the B fragment is the halo row shifted by (dy, dx);
 //   * the activated tile goes to LDS over the halo and the two-phase stage
 //     tail of tpmd_tail.h runs on it (the tail's skips and the folded ToFlow
-//     weights are fetched before the conv).
+//     weights are fetched before the conv; the skips wait in LDS, above the
+//     halo, so that they hold no registers during the conv).
 // One global round trip for the conv instead of one per tap.
 #include "tpmd_conv.h"
 
@@ -35,6 +36,7 @@ struct fused32_cfg {
     static constexpr int WFS = HALO > TAIL ? HALO : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
     static_assert(TH % 4 == 0, "rows per wave");
+    static_assert(HALO <= L::PRM0 * 4, "the tail records lie above the halo");
 };
 
 template <typename TF, typename TT, int TH>
@@ -90,6 +92,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
             *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
         }
     });
+    tile_tail_stash<BN>(prm, tid, sk);  // the records lie above the halo
     __syncthreads();
 
     // conv: acc[b] = 32 channels x the 32 pixels of output row wid*RPW + b
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         });
     });
     __syncthreads();
-    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
+    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, tile_tail_unstash<BN>(prm, tid));
 }
 
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 32 && OC == 32 && r % 32 == 0; }

@@ -204,9 +204,11 @@ __device__ __forceinline__ int tile_pix(int pix0, int r, int p) {
     return pix0 + p;
 }
 
-// upfirdn2x skips of the flow and rgb heads for tile pixel tid (tid < BN)
+// upfirdn2x skips of the flow and rgb heads and the identity-grid
+// coordinates of tile pixel tid (tid < BN)
 struct tail_skip {
     float fl[3], rgb[3];
+    float lx, ly;
 };
 
 template <int BN, int TWC>
@@ -215,11 +217,14 @@ __device__ __forceinline__ tail_skip tile_tail_skips(const TailArgs &a, int n0, 
     tail_skip sk;
 #pragma unroll
     for (int k = 0; k < 3; k++) sk.fl[k] = sk.rgb[k] = 0.0f;
-    if (tid < BN && (a.flow_prev || a.rgb_prev)) {
+    sk.lx = sk.ly = 0.0f;
+    if (tid < BN) {
         const int r = a.r, rh = r >> 1, RR = r * r;
         const int fr = n0 / RR;
         const int pix = tile_pix<TWC>(n0 - fr * RR, r, tid);
         const int y = pix / r, x = pix - y * r;
+        sk.lx = a.lin[x];
+        sk.ly = a.lin[y];
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             if (a.flow_prev)
@@ -227,6 +232,26 @@ __device__ __forceinline__ tail_skip tile_tail_skips(const TailArgs &a, int n0, 
             if (a.rgb_prev)
                 sk.rgb[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
         }
+    }
+    return sk;
+}
+
+// park tile pixel tid's skips in its LDS record (prm, [BN][8] floats) while
+// the conv runs, and take them back before phase 1 overwrites the record
+template <int BN>
+__device__ __forceinline__ void tile_tail_stash(float *prm, int tid, const tail_skip &sk) {
+    if (tid < BN) {
+        *(floatx4 *) (prm + tid * 8) = floatx4{sk.fl[0], sk.fl[1], sk.fl[2], sk.lx};
+        *(floatx4 *) (prm + tid * 8 + 4) = floatx4{sk.ly, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
+    }
+}
+template <int BN>
+__device__ __forceinline__ tail_skip tile_tail_unstash(const float *prm, int tid) {
+    tail_skip sk{};
+    if (tid < BN) {
+        const floatx4 a = *(const floatx4 *) (prm + tid * 8), b = *(const floatx4 *) (prm + tid * 8 + 4);
+        sk.fl[0] = a[0]; sk.fl[1] = a[1]; sk.fl[2] = a[2]; sk.lx = a[3];
+        sk.ly = b[0]; sk.rgb[0] = b[1]; sk.rgb[1] = b[2]; sk.rgb[2] = b[3];
     }
     return sk;
 }
@@ -298,8 +323,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
 #pragma unroll
             for (int k = 0; k < 3; k++) a.flow_cur[((int64_t) fr * 3 + k) * RR + pix] = fl[k];
         }
-        const float gx = tanhf(fl[0]) + a.lin[x];
-        const float gy = tanhf(fl[1]) + a.lin[y];
+        const float gx = tanhf(fl[0]) + sk.lx;
+        const float gy = tanhf(fl[1]) + sk.ly;
         const float m = 1.0f / (1.0f + expf(-fl[2]));
         const taps4 t = gather_geometry(gx, gy, r, r);
         *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
