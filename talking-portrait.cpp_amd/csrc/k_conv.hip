@@ -420,6 +420,8 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (fused && (c.mode != MODE_DENSE || c.H != c.W || c.tail->C != c.OC || c.tail->r != c.H ||
                   (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
         return hipErrorInvalidValue;
+    if (!fused && modconv_up64_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W))
+        return launch_modconv_up64(p, st);
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
     if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H))
