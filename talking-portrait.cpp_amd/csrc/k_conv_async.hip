@@ -37,7 +37,10 @@ template <int BM, int BN, int S>
 struct async_cfg {
     static constexpr int RB = 64;                    // bytes per k-tile row
     static constexpr int STAGE = (BM + BN) * RB;     // bytes per stage
-    static constexpr int LDS = S * STAGE;
+    static constexpr int RING = S * STAGE;
+    static constexpr int ORS = BM * 2 + 16;          // staged f16 output row (one pixel), padded
+    static constexpr int OUT = BN * ORS;
+    static constexpr int LDS = RING > OUT ? RING : OUT;
 };
 
 template <typename TO, int BM, int BN, int WM, int WN, int S, int MODE, int EPI>
@@ -187,24 +190,91 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_async_kernel(ConvParam
     }
 
     // accumulator (a, b, v): row = a*32 + (v/4)*8 + (lane/32)*4 + v%4, col = b*32 + lane%32
-    static_for<TN>([&](auto b) {
-        const int n = n0 + wn * WTN + b * 32 + lrow;
-        if (n < p.N) {
+    if constexpr (EPI == EPI_STORE && sizeof(TO) == 2) {
+        // f16 store epilogue through LDS: the activated tile is staged as
+        // [pixel][row] and written back as whole 16-byte chunks, so a wave
+        // store covers 1 KB of contiguous output instead of 8-byte pieces
+        __syncthreads();  // every wave is done with the ring
+        static_for<TN>([&](auto b) {
+            const int nl = wn * WTN + b * 32 + lrow;
+            const int n = n0 + nl < p.N ? n0 + nl : p.N - 1;
+            const int fr = n / HW;
             static_for<TM>([&](auto a) {
                 static_for<4>([&](auto i) {
-                    const int m = m0 + wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
-                    const float q[4] = {acc[a][b][i * 4], acc[a][b][i * 4 + 1], acc[a][b][i * 4 + 2],
-                                        acc[a][b][i * 4 + 3]};
-                    if constexpr (EPI == EPI_STORE) {
-                        epi_store_quad<TO, MODE>(p, q, m, n);
-                    } else {
-                        float *w = p.ws + ((int64_t) split * p.N + n) * p.M + m;
-                        *(floatx4 *) w = floatx4{q[0], q[1], q[2], q[3]};
+                    const int ml = wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
+                    const int m = m0 + ml;
+                    const int o = MODE == MODE_DENSE ? m : m % p.OC;
+                    const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + o);
+                    const floatx4 bb = *(const floatx4 *) (p.bias + o);
+                    floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
+                    if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
+                    half4 h;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float v = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                        if (p.out_scale) v *= sc[j];
+                        h[j] = (half_t) v;
                     }
+                    *(half4 *) (smem + nl * C::ORS + ml * 2) = h;
                 });
             });
+        });
+        __syncthreads();
+        // chunk c: pixel n0 + c / (BM/8), rows (c % (BM/8)) * 8 .. +8 of the tile
+        constexpr int CPR = BM / 8, NCH = BN * CPR, STEP = NT / CPR;
+        static_assert(NCH % NT == 0 && NT % CPR == 0, "store pass");
+        const int mc = tid % CPR;
+        const int m = m0 + mc * 8;
+        int cls = 0, o = m;
+        if constexpr (MODE == MODE_SUBPIX) {
+            cls = m / p.OC;
+            o = m - cls * p.OC;
         }
-    });
+        // pixel of this thread's first chunk, then STEP pixels further per pass
+        int nl = tid / CPR;
+        int n = n0 + nl;
+        int fr = n / HW, rem = n - fr * HW;
+        int y = rem / W, x = rem - y * W;
+        half_t *Yp = (half_t *) p.Y;
+        static_for<NCH / NT>([&](auto j) {
+            if (n < p.N) {
+                int64_t opix;
+                if constexpr (MODE == MODE_DENSE) opix = n;
+                else opix = (int64_t) fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
+                const u32x4 v = *(const u32x4 *) (smem + nl * C::ORS + mc * 16);
+                *(u32x4 *) (Yp + opix * p.OC + o) = v;
+            }
+            nl += STEP;
+            n += STEP;
+            x += STEP;
+            while (x >= W) {
+                x -= W;
+                if (++y == H) {
+                    y = 0;
+                    fr++;
+                }
+            }
+        });
+    } else {
+        static_for<TN>([&](auto b) {
+            const int n = n0 + wn * WTN + b * 32 + lrow;
+            if (n < p.N) {
+                static_for<TM>([&](auto a) {
+                    static_for<4>([&](auto i) {
+                        const int m = m0 + wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
+                        const float q[4] = {acc[a][b][i * 4], acc[a][b][i * 4 + 1], acc[a][b][i * 4 + 2],
+                                            acc[a][b][i * 4 + 3]};
+                        if constexpr (EPI == EPI_STORE) {
+                            epi_store_quad<TO, MODE>(p, q, m, n);
+                        } else {
+                            float *w = p.ws + ((int64_t) split * p.N + n) * p.M + m;
+                            *(floatx4 *) w = floatx4{q[0], q[1], q[2], q[3]};
+                        }
+                    });
+                });
+            }
+        });
+    }
 }
 
 // ---------------------------------------------------------------------------
