@@ -38,28 +38,43 @@ __global__ __launch_bounds__(256) void style_gemv_kernel(const float *__restrict
         w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
     }
     const float bias = bm[row];
-    for (int f = 0; f < nframes; f++) {
-        const float *l = lat + (int64_t) f * 512 + lane * 8;
-        const floatx4 a = *(const floatx4 *) l, b = *(const floatx4 *) (l + 4);
-        float acc = w[0] * a[0];
-        acc = __builtin_fmaf(w[1], a[1], acc);
-        acc = __builtin_fmaf(w[2], a[2], acc);
-        acc = __builtin_fmaf(w[3], a[3], acc);
-        acc = __builtin_fmaf(w[4], b[0], acc);
-        acc = __builtin_fmaf(w[5], b[1], acc);
-        acc = __builtin_fmaf(w[6], b[2], acc);
-        acc = __builtin_fmaf(w[7], b[3], acc);
-        acc = group_sum<64>(acc);
-        if (lane == 0) s[seg.out0[sg] + (int64_t) f * width + i] = acc + bias;
+    // the latents of FB frames are requested together, then reduced
+    constexpr int FB = 8;
+    for (int f0 = 0; f0 < nframes; f0 += FB) {
+        floatx4 la[FB], lb[FB];
+#pragma unroll
+        for (int k = 0; k < FB; k++) {
+            const int f = f0 + k < nframes ? f0 + k : nframes - 1;
+            const float *l = lat + (int64_t) f * 512 + lane * 8;
+            la[k] = *(const floatx4 *) l;
+            lb[k] = *(const floatx4 *) (l + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < FB; k++) {
+            const floatx4 a = la[k], b = lb[k];
+            float acc = w[0] * a[0];
+            acc = __builtin_fmaf(w[1], a[1], acc);
+            acc = __builtin_fmaf(w[2], a[2], acc);
+            acc = __builtin_fmaf(w[3], a[3], acc);
+            acc = __builtin_fmaf(w[4], b[0], acc);
+            acc = __builtin_fmaf(w[5], b[1], acc);
+            acc = __builtin_fmaf(w[6], b[2], acc);
+            acc = __builtin_fmaf(w[7], b[3], acc);
+            acc = group_sum<64>(acc);
+            if (lane == k && f0 + k < nframes) s[seg.out0[sg] + (int64_t) (f0 + k) * width + i] = acc + bias;
+        }
     }
 }
 
-// one wave per (conv, output channel): den = sqrt(sum_i S[o][i] s_i^2 + S[o][IC])
+// one wave per (conv, output channel): den = sqrt(sum_i S[o][i] s_i^2 + S[o][IC]),
+// FB frames at a time (each lane's partial sums over i = lane, lane+64, ...
+// then the 64-lane butterfly, per frame)
 __global__ __launch_bounds__(256) void demod_kernel(const float *__restrict__ saug,
                                                     const float *__restrict__ s,
                                                     float *__restrict__ inv_den, DemodTable t,
                                                     int nframes) {
 #pragma clang fp contract(off)
+    constexpr int FB = 8;
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= t.row0[t.n]) return;
@@ -68,18 +83,55 @@ __global__ __launch_bounds__(256) void demod_kernel(const float *__restrict__ sa
     const int o = row - t.row0[c];
     const int IC = t.ic[c], OC = t.oc[c];
     const float *S = saug + t.saug0[c] + (int64_t) o * (IC + 1);
-    for (int f = 0; f < nframes; f++) {
-        const float *sv = s + t.s0[c] + (int64_t) f * IC;
-        float acc = 0.0f;
-        for (int i = lane; i < IC; i += 64) {
-            const float si = sv[i];
-            const float s2 = si * si;
-            acc = __builtin_fmaf(S[i], s2, acc);
+    // IC <= 512: the row's weights and each frame block's styles are all
+    // requested before the first multiply-add (one memory round trip each)
+    constexpr int JM = 8;
+    const bool small = IC <= 64 * JM;
+    float w[JM];
+#pragma unroll
+    for (int j = 0; j < JM; j++) w[j] = small && lane + 64 * j < IC ? S[lane + 64 * j] : 0.0f;
+    for (int f0 = 0; f0 < nframes; f0 += FB) {
+        float acc[FB];
+#pragma unroll
+        for (int k = 0; k < FB; k++) acc[k] = 0.0f;
+        const float *sv = s + t.s0[c] + (int64_t) f0 * IC;
+        if (small) {
+            float sx[FB][JM];
+#pragma unroll
+            for (int k = 0; k < FB; k++)
+#pragma unroll
+                for (int j = 0; j < JM; j++)
+                    sx[k][j] = f0 + k < nframes && lane + 64 * j < IC ? sv[(int64_t) k * IC + lane + 64 * j] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < FB; k++)
+#pragma unroll
+                for (int j = 0; j < JM; j++) {
+                    if (lane + 64 * j < IC) {
+                        const float s2 = sx[k][j] * sx[k][j];
+                        acc[k] = __builtin_fmaf(w[j], s2, acc[k]);
+                    }
+                }
+        } else {
+            for (int i = lane; i < IC; i += 64) {
+                const float wi = S[i];
+#pragma unroll
+                for (int k = 0; k < FB; k++) {
+                    if (f0 + k < nframes) {
+                        const float si = sv[(int64_t) k * IC + i];
+                        const float s2 = si * si;
+                        acc[k] = __builtin_fmaf(wi, s2, acc[k]);
+                    }
+                }
+            }
         }
-        acc = group_sum<64>(acc);
-        if (lane == 0) {
-            const float den = sqrtf(acc + S[IC]);
-            inv_den[t.d0[c] + (int64_t) f * OC + o] = 1.0f / den;
+        const float tail = S[IC];
+#pragma unroll
+        for (int k = 0; k < FB; k++) {
+            const float sum = group_sum<64>(acc[k]);
+            if (lane == k && f0 + k < nframes) {
+                const float den = sqrtf(sum + tail);
+                inv_den[t.d0[c] + (int64_t) (f0 + k) * OC + o] = 1.0f / den;
+            }
         }
     }
 }
