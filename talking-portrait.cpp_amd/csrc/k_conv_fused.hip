@@ -61,23 +61,23 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
     const int y0 = ty * TH, x0 = tx * TW;
     const int n0 = (fr * H + y0) * W + x0;  // top-left pixel of the block
 
-    // conv-independent tail inputs
-    const tail_skip sk = tile_tail_skips<BN, TW>(ta, n0, tid);
-    tile_tail_wfs<C, NT>(ta, wfs, fr, tid);
-
-    // halo and A fragments -> registers (one round trip)
+    // memory order, bounded by registers: the tail's skips and the halo are
+    // requested together; once the skips are summed (the halo still in
+    // flight) the A fragments and the frame's ToFlow weights follow
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     u32x4 hv[PF];
-    static_for<PF>([&](auto i) {
-        const int ch = tid + i * NT;
-        hv[i] = u32x4{0u, 0u, 0u, 0u};
-        if (ch < HCH) {
-            const int px = ch / CPP, c = ch - px * CPP;
-            const int hy = px / HWD, hx = px - hy * HWD;
-            const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-            if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
-                hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
-        }
+    const tail_skip sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
+        static_for<PF>([&](auto i) {
+            const int ch = tid + i * NT;
+            hv[i] = u32x4{0u, 0u, 0u, 0u};
+            if (ch < HCH) {
+                const int px = ch / CPP, c = ch - px * CPP;
+                const int hy = px / HWD, hx = px - hy * HWD;
+                const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
+                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
+                    hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
+            }
+        });
     });
     const int lrow = lane & 31, khalf = lane >> 5;
     u32x4 af[NAF];
@@ -85,6 +85,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         const TA *arow = (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
         static_for<NAF>([&](auto j) { af[j] = *(const u32x4 *) (arow + j * 16); });
     }
+    const tail_wfs_regs<C, NT> wr = tile_tail_wfs_load<C, NT>(ta, fr, tid);
     static_for<PF>([&](auto i) {
         const int ch = tid + i * NT;
         if (ch < HCH) {
@@ -92,6 +93,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
             *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
         }
     });
+    tile_tail_wfs_store<C, NT>(wfs, tid, wr);
     tile_tail_stash<BN>(prm, tid, sk);  // the records lie above the halo
     __syncthreads();
 

@@ -79,25 +79,47 @@ __device__ __forceinline__ float group_sum(float v) {
 // i in {X&1, X&1 + 2}, j in {Y&1, Y&1 + 2}, i.e. source columns
 // (X + (X&1) - 2)/2 + {0, 1} and the same for rows.  They are visited in
 // the reference loop's order (j-major, i-minor, out-of-map taps skipped), so
-// the sum equals the 16-tap loop's bit for bit.
-__device__ __forceinline__ float upfirdn2x_at(const float *__restrict__ plane, int W, int H,
-                                              const float *__restrict__ k4, int X, int Y) {
-#pragma clang fp contract(off)
+// the sum equals the 16-tap loop's bit for bit.  The four loads use clamped
+// (always in-map) indices; an out-of-map tap leaves the sum as it was,
+// exactly as skipping it does.  Split in two so that a caller can request the
+// taps of several planes before summing any of them.
+struct upfirdn_taps {
+    float v[4], k[4];
+    bool in[4];
+};
+__device__ __forceinline__ void upfirdn2x_load(const float *__restrict__ plane, int W, int H,
+                                               const float *__restrict__ k4, int X, int Y, upfirdn_taps &t) {
     const int i0 = X & 1, j0 = Y & 1;
     const int sx0 = (X + i0 - 2) >> 1, sy0 = (Y + j0 - 2) >> 1;
-    float acc = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < 2; jj++) {
         const int sy = sy0 + jj;
-        if (sy < 0 || sy >= H) continue;
+        const int cy = sy < 0 ? 0 : (sy >= H ? H - 1 : sy);
 #pragma unroll
         for (int ii = 0; ii < 2; ii++) {
             const int sx = sx0 + ii;
-            if (sx < 0 || sx >= W) continue;
-            acc += plane[sx + W * sy] * k4[i0 + 2 * ii + 4 * (j0 + 2 * jj)];
+            const int cx = sx < 0 ? 0 : (sx >= W ? W - 1 : sx);
+            t.in[2 * jj + ii] = (unsigned) sy < (unsigned) H && (unsigned) sx < (unsigned) W;
+            t.v[2 * jj + ii] = plane[cx + W * cy];
+            t.k[2 * jj + ii] = k4[i0 + 2 * ii + 4 * (j0 + 2 * jj)];
         }
     }
+}
+__device__ __forceinline__ float upfirdn2x_sum(const upfirdn_taps &t) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // j-major, i-minor
+        const float s = acc + t.v[q] * t.k[q];
+        acc = t.in[q] ? s : acc;
+    }
     return acc;
+}
+__device__ __forceinline__ float upfirdn2x_at(const float *__restrict__ plane, int W, int H,
+                                              const float *__restrict__ k4, int X, int Y) {
+    upfirdn_taps t;
+    upfirdn2x_load(plane, W, H, k4, X, Y, t);
+    return upfirdn2x_sum(t);
 }
 
 // grid_sample (bilinear, zeros, align_corners=False) tap geometry for one

@@ -211,8 +211,17 @@ struct tail_skip {
     float lx, ly;
 };
 
+// ... with more loads (`issue`) requested between the skip taps and their sums
+template <int BN, int TWC, typename F>
+__device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int n0, int tid, F &&issue);
+
 template <int BN, int TWC>
 __device__ __forceinline__ tail_skip tile_tail_skips(const TailArgs &a, int n0, int tid) {
+    return tile_tail_skips_then<BN, TWC>(a, n0, tid, []() {});
+}
+
+template <int BN, int TWC, typename F>
+__device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int n0, int tid, F &&issue) {
 #pragma clang fp contract(off)
     tail_skip sk;
 #pragma unroll
@@ -225,13 +234,23 @@ __device__ __forceinline__ tail_skip tile_tail_skips(const TailArgs &a, int n0, 
         const int y = pix / r, x = pix - y * r;
         sk.lx = a.lin[x];
         sk.ly = a.lin[y];
+        // every tap of the six planes is requested before any sum is formed
+        upfirdn_taps tf[3], tr[3];
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             if (a.flow_prev)
-                sk.fl[k] = upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
+                upfirdn2x_load(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y, tf[k]);
             if (a.rgb_prev)
-                sk.rgb[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+                upfirdn2x_load(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y, tr[k]);
         }
+        issue();
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            if (a.flow_prev) sk.fl[k] = upfirdn2x_sum(tf[k]);
+            if (a.rgb_prev) sk.rgb[k] = upfirdn2x_sum(tr[k]);
+        }
+    } else {
+        issue();
     }
     return sk;
 }
@@ -256,13 +275,35 @@ __device__ __forceinline__ tail_skip tile_tail_unstash(const float *prm, int tid
     return sk;
 }
 
-// folded ToFlow weights of frame fr (gemm_weight: W * s rounded to f32)
+// folded ToFlow weights of frame fr (gemm_weight: W * s rounded to f32),
+// in two halves so that the loads can join an earlier memory round trip
+template <int C, int NT>
+struct tail_wfs_regs {
+    static constexpr int N = (3 * C + NT - 1) / NT;
+    float w[N], s[N];
+};
+template <int C, int NT>
+__device__ __forceinline__ tail_wfs_regs<C, NT> tile_tail_wfs_load(const TailArgs &a, int fr, int tid) {
+    tail_wfs_regs<C, NT> r;
+#pragma unroll
+    for (int j = 0; j < r.N; j++) {
+        const int i = tid + j * NT;
+        r.w[j] = i < 3 * C ? a.wflow[i] : 0.0f;
+        r.s[j] = i < 3 * C ? a.sflow[(int64_t) fr * C + i % C] : 0.0f;
+    }
+    return r;
+}
+template <int C, int NT>
+__device__ __forceinline__ void tile_tail_wfs_store(float *wfs, int tid, const tail_wfs_regs<C, NT> &r) {
+#pragma unroll
+    for (int j = 0; j < r.N; j++) {
+        const int i = tid + j * NT;
+        if (i < 3 * C) wfs[i] = r.w[j] * r.s[j];
+    }
+}
 template <int C, int NT>
 __device__ __forceinline__ void tile_tail_wfs(const TailArgs &a, float *wfs, int fr, int tid) {
-    for (int i = tid; i < 3 * C; i += NT) {
-        const int c = i % C;
-        wfs[i] = a.wflow[i] * a.sflow[(int64_t) fr * C + c];
-    }
+    tile_tail_wfs_store<C, NT>(wfs, tid, tile_tail_wfs_load<C, NT>(a, fr, tid));
 }
 
 // 8 channels of one feature tap, kept in the stored type until used
