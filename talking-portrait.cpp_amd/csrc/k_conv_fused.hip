@@ -4,16 +4,16 @@
 // fetched once per tile instead of once per tap:
 //
 //   * a workgroup owns a TH x 32 block of output pixels of one frame; the
-//     (TH+2) x 34 input pixels around it (zero outside the map) are loaded
-//     into registers with the 32 x 288 weight matrix's MFMA A fragments
-//     (18 per lane, kept for the whole conv), then the halo goes to LDS with
-//     a 16-byte pad per pixel (conflict-free 32-pixel fragment reads);
+//     (TH+2) x 34 input pixels around it (zero outside the map) go through
+//     registers to LDS with a 16-byte pad per pixel (conflict-free 32-pixel
+//     fragment reads); the 32 x 288 weight matrix goes global -> LDS by the
+//     DMA path in MFMA fragment order (18 fragments of 1 KB, each read back
+//     by one ds_read_b128 per lane), so it holds no registers;
 //   * wave w computes rows w*TH/4 .. of the block: for each tap (dy, dx) and
 //     16-channel step, the B fragment is the halo row shifted by (dy, dx);
 //   * the activated tile goes to LDS over the halo and the two-phase stage
 //     tail of tpmd_tail.h runs on it (the tail's skips and the folded ToFlow
-//     weights are fetched before the conv; the skips wait in LDS, above the
-//     halo, so that they hold no registers during the conv).
+//     weights are fetched with the halo, in one round trip).
 // One global round trip for the conv instead of one per tap.
 #include "tpmd_conv.h"
 
@@ -32,11 +32,12 @@ struct fused32_cfg {
     static constexpr int RPW = TH / 4;                  // output rows per wave
     typedef tile_tail_lds<C, BN> L;
     static constexpr int HALO = HPX * PXB;
-    static constexpr int TAIL = L::WFS0 * 4;            // so + prm
-    static constexpr int WFS = HALO > TAIL ? HALO : TAIL;
+    static constexpr int AOFF = (HALO + 255) / 256 * 256;  // A fragments, fragment-major
+    static constexpr int CONV = AOFF + NAF * 1024;          // conv-phase LDS
+    static constexpr int TAIL = L::WFS0 * 4;                // so + prm, over the conv's LDS
+    static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
     static_assert(TH % 4 == 0, "rows per wave");
-    static_assert(HALO <= L::PRM0 * 4, "the tail records lie above the halo");
 };
 
 template <typename TF, typename TT, int TH>
@@ -80,10 +81,13 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         });
     });
     const int lrow = lane & 31, khalf = lane >> 5;
-    u32x4 af[NAF];
     {
+        // fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
         const TA *arow = (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
-        static_for<NAF>([&](auto j) { af[j] = *(const u32x4 *) (arow + j * 16); });
+        for (int f = wid; f < NAF; f += NT / 64)
+            __builtin_amdgcn_global_load_lds((const void *) (arow + f * 16),
+                                             (__attribute__((address_space(3))) void *) (smem + F::AOFF + f * 1024),
+                                             16, 0, 0);
     }
     const tail_wfs_regs<C, NT> wr = tile_tail_wfs_load<C, NT>(ta, fr, tid);
     static_for<PF>([&](auto i) {
@@ -94,8 +98,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         }
     });
     tile_tail_wfs_store<C, NT>(wfs, tid, wr);
-    tile_tail_stash<BN>(prm, tid, sk);  // the records lie above the halo
-    __syncthreads();
+    __syncthreads();  // (waits for the A fragments' DMA too)
 
     // conv: acc[b] = 32 channels x the 32 pixels of output row wid*RPW + b
     floatx16 acc[RPW];
@@ -110,9 +113,11 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
                 const int hrow = wid * RPW + b + dy;
                 const u32x4 bf =
                     *(const u32x4 *) (smem + (hrow * HWD + lrow + dx) * PXB + (ks * 2 + khalf) * 16);
-                mfma_op<TA>::run(af[tap * KS + ks], bf, acc[b]);
+                const u32x4 af = *(const u32x4 *) (smem + F::AOFF + (tap * KS + ks) * 1024 + lane * 16);
+                mfma_op<TA>::run(af, bf, acc[b]);
             });
         });
+        __builtin_amdgcn_sched_barrier(0);  // bound the fragments in flight (registers)
     });
     __syncthreads();  // halo reads done: the LDS becomes the activated tile
 
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         });
     });
     __syncthreads();
-    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, tile_tail_unstash<BN>(prm, tid));
+    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
 }
 
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 32 && OC == 32 && r % 32 == 0; }
