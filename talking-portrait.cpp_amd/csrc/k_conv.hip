@@ -434,8 +434,10 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     const TailArgs ta = fused ? *c.tail : TailArgs{};
     hipError_t e;
     const TileCfg tc = pick_tile(p.M, fused, p.N);
-    if (c.f16 && !fused && tc.bm == 256 && c.IC % 32 == 0) {
-        e = launch_modconv_async(p, c.mode, epi, nsplit, c.out_f16, st);
+    // the ring pays for 256 x 256 tiles, and for split-K launches, whose few
+    // k tiles per workgroup leave the load latency exposed otherwise
+    if (c.f16 && !fused && c.IC % 32 == 0 && (tc.bm == 256 || (tc.bm == 128 && tc.bn == 128 && nsplit > 1))) {
+        e = launch_modconv_async(p, c.mode, epi, nsplit, c.out_f16, tc.bm, st);
     } else if (c.f16) {
         if (fused) {
             e = c.trunk_f16 ? launch_typed<half_t, float, half_t, half_t>(p, c.mode, epi, 1, ta, st)

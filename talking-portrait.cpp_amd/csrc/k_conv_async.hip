@@ -469,11 +469,15 @@ static hipError_t launch_async_cfg(ConvParams p, int mode, int epi, int nsplit, 
     return hipGetLastError();
 }
 
-hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16,
+hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16, int bm,
                                 hipStream_t st) {
-    if (p.M % 256 != 0 || p.IC % 32 != 0) return hipErrorInvalidValue;
-    if (out_f16) return launch_async_cfg<half_t, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
-    return launch_async_cfg<float, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
+    if ((bm != 256 && bm != 128) || p.M % bm != 0 || p.IC % 32 != 0) return hipErrorInvalidValue;
+    if (bm == 256) {
+        if (out_f16) return launch_async_cfg<half_t, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
+        return launch_async_cfg<float, 256, 256, 2, 4, 4>(p, mode, epi, nsplit, st);
+    }
+    if (out_f16) return launch_async_cfg<half_t, 128, 128, 2, 2, 4>(p, mode, epi, nsplit, st);
+    return launch_async_cfg<float, 128, 128, 2, 2, 4>(p, mode, epi, nsplit, st);
 }
 
 template <typename TT, int BM, int BN, int WM, int WN>

@@ -111,9 +111,10 @@ __device__ __forceinline__ void epi_store_quad(const ConvParams &p, const float 
 bool modconv_halo_ok(bool f16, int mode, int IC, int OC, int H, int W, bool tail);
 hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, hipStream_t st);
 
-// k_conv_async.hip: f16 store / split-K convs on 256 x 256 tiles (8 waves)
-// with LDS-DMA operand loads into a 4-stage ring; M % 256 == 0, IC % 32 == 0
-hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16,
+// k_conv_async.hip: f16 store / split-K convs with LDS-DMA operand loads into
+// a 4-stage ring; bm = 256 (256 x 256 tiles, 8 waves) or 128 (128 x 128,
+// 4 waves); M % bm == 0, IC % 32 == 0
+hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16, int bm,
                                 hipStream_t st);
 // k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128}
 // (tiles of 256, 128, 128 pixels of one frame) with the same operand ring
