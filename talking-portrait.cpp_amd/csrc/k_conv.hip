@@ -426,6 +426,8 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
     if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H))
         return launch_modconv_fused32(p, *c.tail, c.trunk_f16, st);
+    if (fused && modconv_fused64_ok(c.f16, c.IC, c.OC, c.H))
+        return launch_modconv_fused64(p, *c.tail, c.trunk_f16, st);
     if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H))
         return launch_modconv_tail_async(p, *c.tail, c.trunk_f16, st);
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);

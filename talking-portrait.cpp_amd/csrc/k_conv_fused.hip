@@ -138,6 +138,167 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
     tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
 }
 
+// ---------------------------------------------------------------------------
+// The 64-channel stage (IC = OC = 64): 4 x 32 blocks (the tail's 128 pixels).
+// The halo goes to LDS through registers as above; the 64 x 576 weight
+// matrix is too large to keep, so it streams through a 2-stage LDS ring by
+// the DMA path, one tap (8 fragments of 1 KB) at a time, shared by the four
+// waves; wave w computes weight rows 32*(w&1) .. +31 for block rows
+// 2*(w>>1) .. +1.
+struct fused64_cfg {
+    static constexpr int C = 64, NT = 256, TH = 4, TW = 32, BN = TH * TW;
+    static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
+    static constexpr int PXB = C * 2 + 16;
+    static constexpr int CPP = C * 2 / 16;
+    static constexpr int HCH = HPX * CPP;
+    static constexpr int PF = (HCH + NT - 1) / NT;
+    static constexpr int KS = C / 16;                   // MFMA k steps per tap
+    static constexpr int FPT = 2 * KS;                  // A fragments per tap (2 row blocks)
+    static constexpr int RPW = 2;                       // block rows per wave
+    typedef tile_tail_lds<C, BN> L;
+    static constexpr int HALO = HPX * PXB;
+    static constexpr int AOFF = (HALO + 255) / 256 * 256;
+    static constexpr int ASTG = FPT * 1024;             // one tap of A
+    static constexpr int CONV = AOFF + 2 * ASTG;
+    static constexpr int TAIL = L::WFS0 * 4;
+    static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
+    static constexpr int LDS = WFS + 3 * C * 4;
+    static_assert(FPT % (NT / 64) == 0, "A fragments per wave");
+};
+
+// s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt not waited on
+constexpr int fused_waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+template <typename TF, typename TT>
+__global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
+                                                          int tiles_frame) {
+    typedef half_t TA;
+    typedef fused64_cfg F;
+    typedef typename F::L L;
+    constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
+    constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, FPT = F::FPT, RPW = F::RPW;
+    constexpr int K = 9 * C;
+    constexpr int APW = FPT / (NT / 64);                // A fragment DMAs per wave per tap
+    __shared__ __attribute__((aligned(16))) char smem[F::LDS];
+    float *so = (float *) smem, *prm = so + L::PRM0, *wfs = (float *) (smem + F::WFS);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int mb = wid & 1, rg = wid >> 1;
+    const int lrow = lane & 31, khalf = lane >> 5;
+    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
+    const int fr = tile / tiles_frame;
+    const int trem = tile - fr * tiles_frame;
+    const int ty = trem / tiles_x, tx = trem - ty * tiles_x;
+    const int H = p.H, W = p.W;
+    const int y0 = ty * F::TH, x0 = tx * TW;
+    const int n0 = (fr * H + y0) * W + x0;
+
+    // A fragment f of tap t (f = step*2 + row block): lane l holds
+    // A[32*(f&1) + l%32][t*64 + (f>>1)*16 + (l/32)*8 .. +8]
+    const TA *Ab = (const TA *) p.A;
+    auto issue_a = [&](int t) {
+        char *stage = smem + F::AOFF + (t & 1) * F::ASTG;
+        static_for<APW>([&](auto j) {
+            const int f = wid * APW + j;
+            const TA *src = Ab + (int64_t) ((f & 1) * 32 + lrow) * K + t * C + (f >> 1) * 16 + khalf * 8;
+            __builtin_amdgcn_global_load_lds((const void *) src,
+                                             (__attribute__((address_space(3))) void *) (stage + f * 1024), 16, 0, 0);
+        });
+    };
+
+    // memory order: skips + halo, then taps 0 and 1 of A and the ToFlow weights
+    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
+    u32x4 hv[PF];
+    const tail_skip sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
+        static_for<PF>([&](auto i) {
+            const int ch = tid + i * NT;
+            hv[i] = u32x4{0u, 0u, 0u, 0u};
+            if (ch < HCH) {
+                const int px = ch / CPP, c = ch - px * CPP;
+                const int hy = px / HWD, hx = px - hy * HWD;
+                const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
+                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
+                    hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
+            }
+        });
+    });
+    issue_a(0);
+    issue_a(1);
+    const tail_wfs_regs<C, NT> wr = tile_tail_wfs_load<C, NT>(ta, fr, tid);
+    static_for<PF>([&](auto i) {
+        const int ch = tid + i * NT;
+        if (ch < HCH) {
+            const int px = ch / CPP, c = ch - px * CPP;
+            *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
+        }
+    });
+    tile_tail_wfs_store<C, NT>(wfs, tid, wr);
+    __builtin_amdgcn_s_waitcnt(fused_waitcnt_vm(0));
+    __syncthreads();  // halo, wfs and both A stages in place
+
+    floatx16 acc[RPW];
+    static_for<RPW>([&](auto b) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[b][v] = 0.0f;
+    });
+    static_for<9>([&](auto tap) {
+        constexpr int dy = tap / 3, dx = tap % 3;
+        if constexpr (tap > 0) {
+            // this wave's part of tap `tap` (its only DMAs in flight) landed ...
+            __builtin_amdgcn_s_waitcnt(fused_waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();  // ... every wave's part, and tap-1's stage is free
+            asm volatile("" ::: "memory");
+            if constexpr (tap + 1 < 9) issue_a(tap + 1);
+        }
+        const char *ast = smem + F::AOFF + (tap & 1) * F::ASTG;
+        static_for<KS>([&](auto s) {
+            const u32x4 af = *(const u32x4 *) (ast + (s * 2 + mb) * 1024 + lane * 16);
+            static_for<RPW>([&](auto b) {
+                const int hrow = rg * RPW + b + dy;
+                const u32x4 bf =
+                    *(const u32x4 *) (smem + (hrow * HWD + lrow + dx) * PXB + (s * 2 + khalf) * 16);
+                mfma_op<TA>::run(af, bf, acc[b]);
+            });
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    __syncthreads();  // halo and A reads done: the LDS becomes the activated tile
+
+    // accumulator (b, v): channel mb*32 + (v/4)*8 + (lane/32)*4 + v%4, tile pixel (rg*2 + b)*32 + lane%32
+    static_for<RPW>([&](auto b) {
+        const int col = (rg * RPW + b) * TW + lrow;
+        static_for<4>([&](auto i) {
+            const int row = mb * 32 + i * 8 + khalf * 4;
+            const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * C + row);
+            const floatx4 bb = *(const floatx4 *) (p.bias + row);
+            floatx4 v;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = leaky(acc[b][i * 4 + j] * id[j] + bb[j]);
+            *(floatx4 *) (so + col * L::SOS + row) = v;
+        });
+    });
+    __syncthreads();
+    tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
+}
+
+bool modconv_fused64_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 64 && OC == 64 && r % 32 == 0; }
+
+hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
+    if (p.IC != 64 || p.OC != 64 || p.M != 64 || p.W % 32 != 0 || p.H % fused64_cfg::TH != 0)
+        return hipErrorInvalidValue;
+    const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / fused64_cfg::TH);
+    const int nframes = p.N / (p.H * p.W);
+    const dim3 grid((unsigned) (nframes * tiles_frame));
+    if (trunk_f16)
+        hipLaunchKernelGGL((conv64_tail_kernel<half_t, half_t>), grid, dim3(256), 0, st, p, ta, tiles_x,
+                           tiles_frame);
+    else
+        hipLaunchKernelGGL((conv64_tail_kernel<half_t, float>), grid, dim3(256), 0, st, p, ta, tiles_x,
+                           tiles_frame);
+    return hipGetLastError();
+}
+
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 32 && OC == 32 && r % 32 == 0; }
 
 hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {

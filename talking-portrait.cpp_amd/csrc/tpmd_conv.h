@@ -127,6 +127,9 @@ hipError_t launch_modconv_up64(const ConvParams &p, hipStream_t st);
 // halo tiles of 8 x 32 pixels (r % 32 == 0)
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r);
 hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
+// ... and for IC = OC = 64 on 4 x 32 halo tiles, A streamed through LDS per tap
+bool modconv_fused64_ok(bool f16, int IC, int OC, int r);
+hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
 hipError_t launch_modconv_tail_async(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
 
 }  // namespace tpmd
