@@ -51,10 +51,13 @@ def copy_probe():
     torch.cuda.synchronize()
 
 
-def fused_tail(oc, r):
+def fused_tail(oc, r, ftype="f16"):
     """stages whose dense conv runs the stage tail in its epilogue: all
-    channels in one conv tile, the tile's pixels in one frame"""
+    channels in one conv tile, the tile's pixels in one frame (256 channels:
+    f16 only)"""
     bn = 256 if oc == 32 else 128
+    if oc == 256:
+        return ftype == "f16" and (r * r) % 128 == 0
     return oc in (32, 64, 128) and (r * r) % bn == 0
 
 
@@ -82,7 +85,7 @@ def stage_costs(ic, oc, nframes, ftype):
         b_tl = (r * r * OC * sa + (nframes * 2 * 3 * (r // 2) ** 2 * 4 if j else 0)
                 + (0 if last else px * OC * sa + px * 3 * 4) + px * 3 * 4)
         f_tl = px * OC * 2 * 6
-        if fused_tail(OC, r):
+        if fused_tail(OC, r, ftype):
             b_dt = px * OC * sa + 9 * OC * OC * sw + b_tl
             slots += [(f"r{r}.upconv", f_up, b_up), (f"r{r}.conv+tail", f_dn + f_tl, b_dt), None]
         else:

@@ -300,7 +300,9 @@ int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
 
 // the dense conv of an r x r stage with OC channels can run the stage tail in
 // its epilogue: one tile holds every channel and its pixels lie in one frame
-bool modconv_fusable(int OC, int r) {
+// (OC = 256: f16 only, on the 256 x 128 ring tile of k_conv_async.hip)
+bool modconv_fusable(int OC, int r, bool f16) {
+    if (OC == 256) return f16 && modconv_tail_async_ok(OC, r);
     if (OC != 32 && OC != 64 && OC != 128) return false;
     const TileCfg tc = pick_tile(OC, true);
     return (r * r) % tc.bn == 0;
@@ -416,7 +418,7 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (c.IC % kal != 0 || c.OC % 32 != 0 || (c.mode != MODE_DENSE && c.mode != MODE_SUBPIX))
         return hipErrorInvalidValue;
     const bool fused = c.tail != nullptr;
-    if (fused && !modconv_fusable(c.OC, c.H) ) return hipErrorInvalidValue;
+    if (fused && !modconv_fusable(c.OC, c.H, c.f16)) return hipErrorInvalidValue;
     if (fused && (c.mode != MODE_DENSE || c.H != c.W || c.tail->C != c.OC || c.tail->r != c.H ||
                   (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
         return hipErrorInvalidValue;

@@ -495,7 +495,7 @@ static hipError_t launch_tail_cfg(ConvParams p, const TailArgs &ta, hipStream_t 
 // k_conv.hip kernel (three workgroups per CU) is faster
 bool modconv_tail_async_ok(int OC, int r) {
     if (OC == 32) return (r * r) % 256 == 0;
-    if (OC == 64) return (r * r) % 128 == 0;
+    if (OC == 64 || OC == 256) return (r * r) % 128 == 0;
     return false;
 }
 
@@ -512,6 +512,10 @@ hipError_t launch_modconv_tail_async(const ConvParams &p, const TailArgs &ta, bo
     if (p.M == 128) {
         if (trunk_f16) return launch_tail_cfg<half_t, 128, 128, 2, 2>(p, ta, st);
         return launch_tail_cfg<float, 128, 128, 2, 2>(p, ta, st);
+    }
+    if (p.M == 256) {
+        if (trunk_f16) return launch_tail_cfg<half_t, 256, 128, 4, 2>(p, ta, st);
+        return launch_tail_cfg<float, 256, 128, 4, 2>(p, ta, st);
     }
     return hipErrorInvalidValue;
 }

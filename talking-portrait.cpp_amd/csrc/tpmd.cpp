@@ -342,7 +342,7 @@ bool check_ctx(tpmd_ctx *c) {
 
 // dense convs whose output channels fit one conv tile run the stage tail in
 // their epilogue (the stage output never goes to HBM)
-bool fused_tail(int oc, int r) { return modconv_fusable(oc, r); }
+bool fused_tail(const tpmd_ctx *c, int oc, int r) { return modconv_fusable(oc, r, c->f16); }
 
 // stage entry points run on the caller's stream; NULL is HIP's null stream
 hipStream_t pick_stream(tpmd_ctx *, void *s) { return (hipStream_t) s; }
@@ -616,7 +616,7 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
     for (int j = 0; j < ns; j++) {
         const size_t r = (size_t) 8 << j;
         act_max = std::max(act_max, r * r * c->oc[j]);
-        if (!fused_tail(c->oc[j], (int) r)) out_max = std::max(out_max, r * r * c->oc[j]);
+        if (!fused_tail(c, c->oc[j], (int) r)) out_max = std::max(out_max, r * r * c->oc[j]);
         if (j + 1 < ns) skip_max = std::max(skip_max, 3 * r * r);
     }
     const size_t R = (size_t) c->out_res();
@@ -765,7 +765,7 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
             return false;
         mark();
         const TailArgs ta = stage_tail_args(c, j, n, img_dst);
-        if (fused_tail(C, r)) {
+        if (fused_tail(c, C, r)) {
             ConvArgs ca = conv_args(c, dn, n, r, c->c1, nullptr, nullptr, false);
             ca.tail = &ta;
             ca.trunk_f16 = f16;
@@ -1109,7 +1109,7 @@ int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float
         ca.ws = (float *) c->scratch(3, (size_t) ca.ws_elems * 4);
         if (!ca.ws) return -1;
     }
-    if (fused_tail(C, r)) {
+    if (fused_tail(c, C, r)) {
         ca.tail = &a;
         return c->hip_ok(launch_modconv(ca, st), "conv+tail") ? 0 : -1;
     }

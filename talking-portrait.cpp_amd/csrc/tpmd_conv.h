@@ -116,8 +116,8 @@ hipError_t launch_modconv_halo(const ConvParams &p, int mode, bool out_f16, hipS
 // 4 waves); M % bm == 0, IC % 32 == 0
 hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nsplit, bool out_f16, int bm,
                                 hipStream_t st);
-// k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128}
-// (tiles of 256, 128, 128 pixels of one frame) with the same operand ring
+// k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128,
+// 256} (tiles of 256, 128, 128, 128 pixels of one frame) with the same ring
 bool modconv_tail_async_ok(int OC, int r);
 // k_conv_up.hip: f16 composed sub-pixel up-conv 64 -> 32 channels with f16
 // output, on 4 x 32 halo tiles (H % 4 == 0, W % 32 == 0)

@@ -86,7 +86,7 @@ struct ConvArgs {
 
 int modconv_k_align(bool f16);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
-bool modconv_fusable(int OC, int r);
+bool modconv_fusable(int OC, int r, bool f16);
 // split-K factor of a conv (depends on the per-frame shape only)
 int modconv_splits(int mode, int H, int W, int IC, int OC, bool f16);
 // workspace floats a conv needs for nframes frames (0 = no split)
