@@ -420,13 +420,6 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
         for (int b = 0; b < NB; b++) {
             const int lp = (it0 + b) * PPB + wid * PPW + grp;
             const int pix = tile_pix<TWC>(pix0, r, lp);
-            float ov[8];
-            {
-                const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
-                const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
-                ov[0] = x0[0]; ov[1] = x0[1]; ov[2] = x0[2]; ov[3] = x0[3];
-                ov[4] = x1[0]; ov[5] = x1[1]; ov[6] = x1[2]; ov[7] = x1[3];
-            }
             // taps and weights exactly as the reference selects them; the
             // weighted sum as one fused multiply-add per channel and tap
             float smp[8];
@@ -438,16 +431,19 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
 #pragma unroll
                 for (int e = 0; e < 8; e++) smp[e] = __builtin_fmaf(wk, fv[b][k][e], smp[e]);
             }
-            float warp[8], trunk[8];
-            const float one_m = 1.0f - m[b];
+            float warp[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                warp[e] = smp[e] * m[b];
-                trunk[e] = warp[e] + ov[e] * one_m;
-            }
+            for (int e = 0; e < 8; e++) warp[e] = smp[e] * m[b];
             const unsigned po = (unsigned) pix * C + c0;
             if (warpf) store8<float>(warpf + po, warp);
-            if (trunkb) {
+            if (trunkb) {  // the last stage has no trunk: the conv output is not read again
+                const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
+                const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
+                const float ov[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                const float one_m = 1.0f - m[b];
+                float trunk[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) trunk[e] = warp[e] + ov[e] * one_m;
                 if (a.s_next) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
