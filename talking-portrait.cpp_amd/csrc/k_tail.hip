@@ -48,6 +48,35 @@ static hipError_t launch_tail_typed(const TailArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// ToRGB weight . feature, per feature pixel: the last stage's ToRGB sum as a
+// bilinear sample of 3 values instead of C (tile_tail, tpmd_tail.h)
+template <typename TF>
+__global__ __launch_bounds__(256) void feat_rgb_kernel(const TF *__restrict__ feat, const float *__restrict__ wrgb,
+                                                       int C, int64_t npix, float *__restrict__ g) {
+    for (int64_t p = (int64_t) blockIdx.x * 256 + threadIdx.x; p < npix; p += (int64_t) gridDim.x * 256) {
+        float acc[3] = {0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < C; c++) {
+            const float f = (float) feat[p * C + c];
+#pragma unroll
+            for (int k = 0; k < 3; k++) acc[k] = __builtin_fmaf(wrgb[k * C + c], f, acc[k]);
+        }
+        *(floatx4 *) (g + p * 4) = floatx4{acc[0], acc[1], acc[2], 0.0f};
+    }
+}
+
+hipError_t launch_feat_rgb(bool feat_f16, const void *feat, const float *wrgb, int C, int64_t npix, float *g,
+                           hipStream_t st) {
+    if (npix <= 0) return hipSuccess;
+    const int64_t nb = (npix + 255) / 256 > 8192 ? 8192 : (npix + 255) / 256;
+    if (feat_f16)
+        hipLaunchKernelGGL(feat_rgb_kernel<half_t>, dim3((unsigned) nb), dim3(256), 0, st, (const half_t *) feat,
+                           wrgb, C, npix, g);
+    else
+        hipLaunchKernelGGL(feat_rgb_kernel<float>, dim3((unsigned) nb), dim3(256), 0, st, (const float *) feat,
+                           wrgb, C, npix, g);
+    return hipGetLastError();
+}
+
 hipError_t launch_stage_tail(const TailArgs &a, bool feat_f16, bool out_f16, bool trunk_f16,
                              hipStream_t st) {
     if (a.nframes <= 0) return hipSuccess;

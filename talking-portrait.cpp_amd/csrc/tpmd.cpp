@@ -51,6 +51,7 @@ struct StageW {
     float *wrgb = nullptr, *rlb = nullptr, *rbias = nullptr, *rup = nullptr;
     float *lin = nullptr;
     void *feat = nullptr;      // act [r*r][oc]
+    float *featg = nullptr;    // [r*r][4] ToRGB weight . feat
     int seg = 0;
     int64_t s_off = 0;
 };
@@ -645,6 +646,10 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
         c->st[j].feat = A(fb);
         if (!c->st[j].feat) return -1;
         if (!c->hip_ok(hipMemset(c->st[j].feat, 0, fb), "memset")) return -1;
+        const size_t gb = r * r * 16 + TAIL_FEATG_PAD;
+        c->st[j].featg = (float *) A(gb);
+        if (!c->st[j].featg) return -1;
+        if (!c->hip_ok(hipMemset(c->st[j].featg, 0, gb), "memset")) return -1;
     }
     c->built = true;
     return 0;
@@ -676,6 +681,9 @@ static int set_feats_impl(tpmd_ctx *c, const float *const *feats, bool dev) {
             return -1;
         if (!c->hip_ok(launch_prescale_map(c->f16, tmp, nullptr, c->st[j].feat, c->oc[j], (int64_t) r * r, 1,
                                            c->stream), "feat convert"))
+            return -1;
+        if (!c->hip_ok(launch_feat_rgb(c->f16, c->st[j].feat, c->st[j].wrgb, c->oc[j], (int64_t) r * r,
+                                       c->st[j].featg, c->stream), "feat rgb"))
             return -1;
         if (!c->hip_ok(hipStreamSynchronize(c->stream), "feat sync")) return -1;
     }
@@ -709,6 +717,7 @@ static TailArgs stage_tail_args(tpmd_ctx *c, int j, int n, float *img_dst) {
     a.s_next = last ? nullptr : c->s_all + c->conv[3 + 2 * j].s_off;
     a.trunk = last ? nullptr : c->trunk;
     a.warp_tap = nullptr;
+    a.featg = a.trunk ? nullptr : s.featg;
     a.nframes = n;
     a.r = 8 << j;
     a.C = c->oc[j];
@@ -1033,6 +1042,7 @@ int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_
     a.s_next = nullptr;
     a.trunk = trunk;
     a.warp_tap = warp;
+    a.featg = trunk || warp ? nullptr : s.featg;
     a.nframes = n;
     a.r = 8 << j;
     a.C = c->oc[j];
@@ -1088,6 +1098,7 @@ int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float
     a.rgb_cur = rgb;
     a.trunk = trunk;
     a.warp_tap = warp;
+    a.featg = trunk || warp ? nullptr : c->st[j].featg;
     a.nframes = n;
     a.r = r;
     a.C = C;

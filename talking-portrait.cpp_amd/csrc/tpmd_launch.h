@@ -26,9 +26,10 @@ struct DemodTable {
     int64_t d0[kMaxSeg];      // element offset of its 1/den block [frame][OC]
 };
 
-// zero bytes that follow every warp feature map: the fused stage tail reads
-// them for the bilinear taps outside the map
+// zero bytes that follow every warp feature map and its ToRGB projection:
+// the fused stage tail reads them for the bilinear taps outside the map
 constexpr int TAIL_FEAT_PAD = 64;
+constexpr int TAIL_FEATG_PAD = 64;
 
 struct TailArgs {
     const void *out;          // CL [frame][r*r][C] dense-conv output (TOUT)
@@ -49,9 +50,16 @@ struct TailArgs {
     const float *s_next;      // [frame][C] style of the next up-conv, or null
     void *trunk;              // CL [frame][r*r][C] (TT) or null
     float *warp_tap;          // CL [frame][r*r][C] f32 or null (tests)
+    // [r*r][4] f32: ToRGB weight . feat of each feature pixel (4th value 0),
+    // then TAIL_FEATG_PAD zero bytes; set only when neither trunk nor
+    // warp_tap is stored, so the warp is needed for the ToRGB sum alone
+    const float *featg;
     int nframes, r, C;
 };
 
+// g[p] = (wrgb[0] . feat[p], wrgb[1] . feat[p], wrgb[2] . feat[p], 0), p < npix
+hipError_t launch_feat_rgb(bool feat_f16, const void *feat, const float *wrgb, int C, int64_t npix, float *g,
+                           hipStream_t st);
 hipError_t launch_gather(const void *feat, bool feat_f16, const float *grid, float *dst, int C,
                          int W, int H, int64_t N, int planar, int sp, hipStream_t st);
 hipError_t launch_gather_taps(const float *grid, int W, int H, int64_t N, int planar, int32_t *x0,

@@ -368,9 +368,42 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
         const float gy = tanhf(fl[1]) + sk.ly;
         const float m = 1.0f / (1.0f + expf(-fl[2]));
         const taps4 t = gather_geometry(gx, gy, r, r);
-        *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
-        *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
+        if (a.featg) {
+            // the warp feeds ToRGB alone: Wr . (m * sum_k w_k feat_k) =
+            // m * sum_k w_k (Wr . feat_k), with Wr . feat stored per feature
+            // pixel; a tap outside the map reads the zero pad after it
+            const char *gb = (const char *) a.featg;
+            const unsigned gpad = (unsigned) RR * 16u;
+            const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) (t.x0 + 1) < (unsigned) r};
+            const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) (t.y0 + 1) < (unsigned) r};
+            const unsigned base = (unsigned) (t.y0 * r + t.x0) * 16u;
+            floatx4 gv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * 16);
+                gv[k] = *(const floatx4 *) (gb + (inx[k & 1] && iny[k >> 1] ? off : gpad));
+            }
+            float rgb[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float wk = tap_weight(t, k);
+#pragma unroll
+                for (int q = 0; q < 3; q++) rgb[q] = __builtin_fmaf(wk, gv[k][q], rgb[q]);
+            }
+            float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
+#pragma unroll
+            for (int q = 0; q < 3; q++) {
+                float v = leaky(rgb[q] * m + a.rlb[q]);
+                v = v + a.rbias[q];
+                if (a.rgb_prev) v = v + sk.rgb[q];
+                rgbf[(unsigned) (q * RR + pix)] = v;
+            }
+        } else {
+            *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
+            *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
+        }
     }
+    if (a.featg) return;  // (uniform) nothing is left for phase 2
     __syncthreads();
 
     // ---- phase 2: G lanes per pixel, 8 channels each; the feature taps of

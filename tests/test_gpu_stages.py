@@ -196,3 +196,11 @@ def test_conv_tail_all_stages(om, torch_cuda, ftype, ic, oc):
                             t["flow"], t["trunk"], t["rgb"], t["warp"])
         for k, w in (("flow", fl), ("warp", warp), ("trunk", trunk), ("rgb", rgb)):
             _check(ftype, t[k].cpu().numpy(), w, (j, k))
+        # neither warp nor trunk stored (the last stage of a decode): ToRGB
+        # from the per-pixel projection of the feature map
+        t2 = {"flow": torch.empty((nf, 3, r, r), device="cuda"), "rgb": torch.empty((nf, 3, r, r), device="cuda")}
+        dec.stage_conv_tail(j, _dev(torch, c1), _dev(torch, s), _dev(torch, fs),
+                            None if skf is None else _dev(torch, skf), None if sk is None else _dev(torch, sk),
+                            t2["flow"], None, t2["rgb"], None)
+        assert torch.equal(t2["flow"], t["flow"]), (j, "flow without warp")
+        _check(ftype, t2["rgb"].cpu().numpy(), rgb, (j, "rgb without warp"))
