@@ -16,122 +16,83 @@ __device__ __forceinline__ int find_seg(const SegTable &t, int row) {
     return s;
 }
 
-// one wave per row: 64 lanes x 8 k-values = the 512-d latent; the row's
-// weights stay in registers while the frames are swept, one butterfly each.
+// Both are skinny GEMMs, Y[f][row] = sum_k W[row][k] X[f][k] over 16 frames,
+// run on v_mfma_f32_16x16x4_f32: one wave owns 16 rows x 16 frames.  Lane l
+// feeds A = W[row0 + l%16][k] and B = X[f0 + l%16][k] for k = kb + 4(l/16) + j,
+// j = 0..3 (one MFMA each: a 16-byte load per operand covers four k steps,
+// the k order inside a 16-wide block permuted the same way for both); the
+// result of lane l, element v is row row0 + 4(l/16) + v, frame f0 + l%16.
+// A frame's sums never mix with another frame's (its own MFMA column).
+__device__ __forceinline__ floatx4 mfma16x4_block(const floatx4 a, const floatx4 b, floatx4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc, 0, 0, 0);
+    return acc;
+}
+
+// style: W = Wmod (all convs' rows, K = 512), X = the latents
 __global__ __launch_bounds__(256) void style_gemv_kernel(const float *__restrict__ Wm,
                                                          const float *__restrict__ bm,
                                                          const float *__restrict__ lat,
                                                          float *__restrict__ s, SegTable seg,
                                                          int nframes) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int R = seg.row0[seg.n];
-    if (row >= R) return;  // whole wave exits together
-    const int sg = find_seg(seg, row);
-    const int i = row - seg.row0[sg];
-    const int width = seg.width[sg];
-    float w[8];
-    {
-        const floatx4 a = *(const floatx4 *) (Wm + (int64_t) row * 512 + lane * 8);
-        const floatx4 b = *(const floatx4 *) (Wm + (int64_t) row * 512 + lane * 8 + 4);
-        w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
-        w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
-    }
-    const float bias = bm[row];
-    // the latents of FB frames are requested together, then reduced
-    constexpr int FB = 8;
-    for (int f0 = 0; f0 < nframes; f0 += FB) {
-        floatx4 la[FB], lb[FB];
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+    if (r0 >= seg.row0[seg.n]) return;  // whole wave exits together
+    const int sg = find_seg(seg, r0);
+    const int li = lane & 15, kq = lane >> 4;
+    const int f0 = blockIdx.y * 16;
+    const int f = f0 + li < nframes ? f0 + li : nframes - 1;
+    const float *wp = Wm + (int64_t) (r0 + li) * 512 + kq * 4;
+    const float *xp = lat + (int64_t) f * 512 + kq * 4;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (int kb = 0; kb < 512; kb += 16)
+        acc = mfma16x4_block(*(const floatx4 *) (wp + kb), *(const floatx4 *) (xp + kb), acc);
+    if (f0 + li < nframes) {
+        const int width = seg.width[sg];
+        float *out = s + seg.out0[sg] + (int64_t) (f0 + li) * width + (r0 - seg.row0[sg]) + kq * 4;
 #pragma unroll
-        for (int k = 0; k < FB; k++) {
-            const int f = f0 + k < nframes ? f0 + k : nframes - 1;
-            const float *l = lat + (int64_t) f * 512 + lane * 8;
-            la[k] = *(const floatx4 *) l;
-            lb[k] = *(const floatx4 *) (l + 4);
-        }
-#pragma unroll
-        for (int k = 0; k < FB; k++) {
-            const floatx4 a = la[k], b = lb[k];
-            float acc = w[0] * a[0];
-            acc = __builtin_fmaf(w[1], a[1], acc);
-            acc = __builtin_fmaf(w[2], a[2], acc);
-            acc = __builtin_fmaf(w[3], a[3], acc);
-            acc = __builtin_fmaf(w[4], b[0], acc);
-            acc = __builtin_fmaf(w[5], b[1], acc);
-            acc = __builtin_fmaf(w[6], b[2], acc);
-            acc = __builtin_fmaf(w[7], b[3], acc);
-            acc = group_sum<64>(acc);
-            if (lane == k && f0 + k < nframes) s[seg.out0[sg] + (int64_t) (f0 + k) * width + i] = acc + bias;
-        }
+        for (int v = 0; v < 4; v++) out[v] = acc[v] + bm[r0 + kq * 4 + v];
     }
 }
 
-// one wave per (conv, output channel): den = sqrt(sum_i S[o][i] s_i^2 + S[o][IC]),
-// FB frames at a time (each lane's partial sums over i = lane, lane+64, ...
-// then the 64-lane butterfly, per frame)
+// demod: den = sqrt(sum_i S[o][i] s_i^2 + S_tail[o]) per (demod conv, output
+// channel o), W = S_aug rows of the conv, X = its styles squared
 __global__ __launch_bounds__(256) void demod_kernel(const float *__restrict__ saug,
                                                     const float *__restrict__ s,
                                                     float *__restrict__ inv_den, DemodTable t,
                                                     int nframes) {
 #pragma clang fp contract(off)
-    constexpr int FB = 8;
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= t.row0[t.n]) return;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+    if (r0 >= t.row0[t.n]) return;
     int c = 0;
-    while (c + 1 < t.n && row >= t.row0[c + 1]) c++;
-    const int o = row - t.row0[c];
+    while (c + 1 < t.n && r0 >= t.row0[c + 1]) c++;
+    const int o0 = r0 - t.row0[c];
     const int IC = t.ic[c], OC = t.oc[c];
-    const float *S = saug + t.saug0[c] + (int64_t) o * (IC + 1);
-    // IC <= 512: the row's weights and each frame block's styles are all
-    // requested before the first multiply-add (one memory round trip each)
-    constexpr int JM = 8;
-    const bool small = IC <= 64 * JM;
-    float w[JM];
+    const float *S = saug + t.saug0[c];
+    const int li = lane & 15, kq = lane >> 4;
+    const int f0 = blockIdx.y * 16;
+    const int f = f0 + li < nframes ? f0 + li : nframes - 1;
+    const float *wp = S + (int64_t) (o0 + li) * IC + kq * 4;
+    const float *xp = s + t.s0[c] + (int64_t) f * IC + kq * 4;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int kb = 0; kb < IC; kb += 16) {
+        const floatx4 x = *(const floatx4 *) (xp + kb);
+        floatx4 x2;
 #pragma unroll
-    for (int j = 0; j < JM; j++) w[j] = small && lane + 64 * j < IC ? S[lane + 64 * j] : 0.0f;
-    for (int f0 = 0; f0 < nframes; f0 += FB) {
-        float acc[FB];
+        for (int j = 0; j < 4; j++) x2[j] = x[j] * x[j];
+        acc = mfma16x4_block(*(const floatx4 *) (wp + kb), x2, acc);
+    }
+    if (f0 + li < nframes) {
+        float *out = inv_den + t.d0[c] + (int64_t) (f0 + li) * OC + o0 + kq * 4;
 #pragma unroll
-        for (int k = 0; k < FB; k++) acc[k] = 0.0f;
-        const float *sv = s + t.s0[c] + (int64_t) f0 * IC;
-        if (small) {
-            float sx[FB][JM];
-#pragma unroll
-            for (int k = 0; k < FB; k++)
-#pragma unroll
-                for (int j = 0; j < JM; j++)
-                    sx[k][j] = f0 + k < nframes && lane + 64 * j < IC ? sv[(int64_t) k * IC + lane + 64 * j] : 0.0f;
-#pragma unroll
-            for (int k = 0; k < FB; k++)
-#pragma unroll
-                for (int j = 0; j < JM; j++) {
-                    if (lane + 64 * j < IC) {
-                        const float s2 = sx[k][j] * sx[k][j];
-                        acc[k] = __builtin_fmaf(w[j], s2, acc[k]);
-                    }
-                }
-        } else {
-            for (int i = lane; i < IC; i += 64) {
-                const float wi = S[i];
-#pragma unroll
-                for (int k = 0; k < FB; k++) {
-                    if (f0 + k < nframes) {
-                        const float si = sv[(int64_t) k * IC + i];
-                        const float s2 = si * si;
-                        acc[k] = __builtin_fmaf(wi, s2, acc[k]);
-                    }
-                }
-            }
-        }
-        const float tail = S[IC];
-#pragma unroll
-        for (int k = 0; k < FB; k++) {
-            const float sum = group_sum<64>(acc[k]);
-            if (lane == k && f0 + k < nframes) {
-                const float den = sqrtf(sum + tail);
-                inv_den[t.d0[c] + (int64_t) (f0 + k) * OC + o] = 1.0f / den;
-            }
+        for (int v = 0; v < 4; v++) {
+            const float den = sqrtf(acc[v] + S[(int64_t) OC * IC + o0 + kq * 4 + v]);
+            out[v] = 1.0f / den;
         }
     }
 }
@@ -167,12 +128,16 @@ __global__ __launch_bounds__(256) void prescale_map_kernel(const float *__restri
     }
 }
 
+// 16-row tiles: every segment starts and ends on a multiple of 16 rows
 hipError_t launch_style_gemv(const float *Wm, const float *bm, const float *lat, float *s,
                              const SegTable &seg, int nframes, hipStream_t st) {
     const int R = seg.row0[seg.n];
     if (R <= 0 || nframes <= 0) return hipSuccess;
-    hipLaunchKernelGGL(style_gemv_kernel, dim3((R + 3) / 4), dim3(256), 0, st, Wm, bm, lat, s, seg,
-                       nframes);
+    for (int i = 0; i <= seg.n; i++)
+        if (seg.row0[i] % 16 != 0) return hipErrorInvalidValue;
+    const int tiles = R / 16;
+    hipLaunchKernelGGL(style_gemv_kernel, dim3((tiles + 3) / 4, (nframes + 15) / 16), dim3(256), 0, st, Wm, bm,
+                       lat, s, seg, nframes);
     return hipGetLastError();
 }
 
@@ -180,8 +145,13 @@ hipError_t launch_demod(const float *saug, const float *s, float *inv_den, const
                         int nframes, hipStream_t st) {
     const int R = t.row0[t.n];
     if (R <= 0 || nframes <= 0) return hipSuccess;
-    hipLaunchKernelGGL(demod_kernel, dim3((R + 3) / 4), dim3(256), 0, st, saug, s, inv_den, t,
-                       nframes);
+    for (int i = 0; i < t.n; i++)
+        if (t.row0[i] % 16 != 0 || t.ic[i] % 16 != 0 || t.oc[i] % 16 != 0 || t.saug0[i] % 4 != 0 ||
+            t.s0[i] % 4 != 0)
+            return hipErrorInvalidValue;
+    const int tiles = R / 16;
+    hipLaunchKernelGGL(demod_kernel, dim3((tiles + 3) / 4, (nframes + 15) / 16), dim3(256), 0, st, saug, s,
+                       inv_den, t, nframes);
     return hipGetLastError();
 }
 

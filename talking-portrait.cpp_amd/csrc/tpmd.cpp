@@ -315,8 +315,9 @@ std::vector<float> make_tsub(const std::vector<float> &W, const std::vector<floa
     return t;
 }
 
-// S_aug [OC][IC+1]: 0.5*sum_k W^2 (double), last column 0.5e-8
-// (src/motion_dec.cpp:113-122): folds the FusedLeakyReLU sqrt2 into 1/den
+// S_aug (src/motion_dec.cpp:113-122): [OC][IC] 0.5*sum_k W^2 (double), then
+// the [OC] last column 0.5e-8 (folds the FusedLeakyReLU sqrt2 into 1/den);
+// rows of IC floats keep every row 16-byte aligned for the demod kernel
 std::vector<float> make_saug(const std::vector<float> &W, int OC, int IC) {
     std::vector<float> s((size_t) OC * (IC + 1));
     for (int o = 0; o < OC; o++) {
@@ -324,9 +325,9 @@ std::vector<float> make_saug(const std::vector<float> &W, int OC, int IC) {
             double a = 0;
             const float *w = W.data() + ((size_t) o * IC + i) * 9;
             for (int k = 0; k < 9; k++) a += (double) w[k] * w[k];
-            s[(size_t) o * (IC + 1) + i] = (float) (a * 0.5);
+            s[(size_t) o * IC + i] = (float) (a * 0.5);
         }
-        s[(size_t) o * (IC + 1) + IC] = 0.5e-8f;
+        s[(size_t) OC * IC + o] = 0.5e-8f;
     }
     return s;
 }

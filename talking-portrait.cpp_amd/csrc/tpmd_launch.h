@@ -21,7 +21,7 @@ struct DemodTable {
     int n;
     int row0[kMaxSeg + 1];
     int ic[kMaxSeg], oc[kMaxSeg];
-    int64_t saug0[kMaxSeg];   // element offset of the conv's S_aug [OC][IC+1]
+    int64_t saug0[kMaxSeg];   // element offset of the conv's S_aug: [OC][IC], then [OC]
     int64_t s0[kMaxSeg];      // element offset of its style block [frame][IC]
     int64_t d0[kMaxSeg];      // element offset of its 1/den block [frame][OC]
 };
