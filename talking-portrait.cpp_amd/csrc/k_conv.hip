@@ -298,6 +298,10 @@ static int row_bytes(int IC, int esize) { return (IC * esize) % 128 == 0 ? 128 :
 
 int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
 
+bool modconv_uses_chunk_A(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
+    return modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W);
+}
+
 // the dense conv of an r x r stage with OC channels can run the stage tail in
 // its epilogue: one tile holds every channel and its pixels lie in one frame
 // (OC = 256: f16 only, on the 256 x 128 ring tile of k_conv_async.hip)
@@ -424,6 +428,12 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
         return hipErrorInvalidValue;
     if (!fused && modconv_up64_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W))
         return launch_modconv_up64(p, st);
+    // (the decoder supplies A_chunk for every conv whose decode shape this
+    // accepts; a test entry at another shape may run the tap-major kernels)
+    if (!fused && c.A_chunk && modconv_hring_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
+        p.A = c.A_chunk;
+        return launch_modconv_hring(p, c.mode, st);
+    }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
     if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H))

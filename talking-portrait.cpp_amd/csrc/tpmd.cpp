@@ -40,6 +40,7 @@ struct ConvW {
     int ic = 0, oc = 0;
     bool up = false;
     void *A = nullptr;         // act [M][9*IC], M = oc or 4*oc
+    void *A_chunk = nullptr;   // act [M][IC/32][9][32]: A in channel-chunk-major k order, or null
     float *bias = nullptr;     // [oc] activate.bias (x sqrt2)
     int64_t saug_off = 0;      // into saug_all, [oc][ic+1]
     int seg = 0;               // style segment
@@ -332,6 +333,18 @@ std::vector<float> make_saug(const std::vector<float> &W, int OC, int IC) {
     return s;
 }
 
+// A [M][9*IC] (k = tap*IC + ic) -> [M][IC/32][9][32] (k = (ic/32*9 + tap)*32 + ic%32)
+std::vector<float> chunk_major(const std::vector<float> &A, int M, int IC) {
+    const size_t K = (size_t) 9 * IC;
+    std::vector<float> out(A.size());
+    for (int m = 0; m < M; m++)
+        for (int c = 0; c < IC / 32; c++)
+            for (int tap = 0; tap < 9; tap++)
+                for (int i = 0; i < 32; i++)
+                    out[m * K + ((size_t) c * 9 + tap) * 32 + i] = A[m * K + (size_t) tap * IC + c * 32 + i];
+    return out;
+}
+
 bool check_ctx(tpmd_ctx *c) {
     if (!c) return false;
     c->err.clear();
@@ -499,15 +512,23 @@ int tpmd_prepare(tpmd_ctx *c) {
         std::vector<float> sa = make_saug(W->data, cv.oc, cv.ic);
         cv.saug_off = (int64_t) saug_all.size();
         saug_all.insert(saug_all.end(), sa.begin(), sa.end());
+        std::vector<float> A;
         if (cv.up) {
             const HostTensor *bk = c->need(base + ".conv.blur.kernel");
             if (!bk) return -1;
-            cv.A = c->upload_act(make_tsub(W->data, bk->data, cv.oc, cv.ic));
+            A = make_tsub(W->data, bk->data, cv.oc, cv.ic);
         } else {
             // conv1 uses its weight tensor as stored (f16-kept values); the
             // dense convs use the derived acf (f16 whenever ftype is f16)
             std::vector<float> wv = L == 0 ? c->dev_value(*W) : W->data;
-            cv.A = c->upload_act(make_acf(wv, cv.oc, cv.ic));
+            A = make_acf(wv, cv.oc, cv.ic);
+        }
+        cv.A = c->upload_act(A);
+        // input map of the conv: 4 x 4 for conv1, r/2 for stage j's up-conv, r for its dense conv
+        const int hin = L == 0 ? 4 : (cv.up ? 4 << j : 8 << j);
+        if (modconv_uses_chunk_A(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin)) {
+            cv.A_chunk = c->upload_act(chunk_major(A, cv.up ? 4 * cv.oc : cv.oc, cv.ic));
+            if (!cv.A_chunk) return -1;
         }
         cv.bias = c->upload(ab->data);
         if (!cv.A || !cv.bias) return -1;
@@ -732,6 +753,7 @@ static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void
     a.f16 = c->f16;
     a.out_f16 = out_f16;
     a.A = cv.A;
+    a.A_chunk = cv.A_chunk;
     a.X = X;
     a.Y = Y;
     a.inv_den = c->den_all + cv.d_off;
@@ -988,6 +1010,7 @@ int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, con
     ca.mode = cv.up ? 1 : 0;
     ca.f16 = c->f16;
     ca.A = cv.A;
+    ca.A_chunk = cv.A_chunk;
     ca.X = xs;
     ca.Y = y;
     ca.inv_den = den;
@@ -1107,6 +1130,7 @@ int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float
     ca.mode = 0;
     ca.f16 = c->f16;
     ca.A = cv.A;
+    ca.A_chunk = cv.A_chunk;
     ca.X = xs;
     ca.inv_den = den;
     ca.bias = cv.bias;

@@ -77,6 +77,7 @@ struct ConvArgs {
     bool f16 = false;           // operands f16 (else f32)
     bool out_f16 = false;       // stored activation f16 (f16 mode only)
     const void *A = nullptr;    // [M][9*IC], M = OC or 4*OC
+    const void *A_chunk = nullptr;  // the same in [M][IC/32][9][32] order, or null (modconv_uses_chunk_A)
     const void *X = nullptr;    // CL input [frame][H][W][IC], frame stride x_bstride
     void *Y = nullptr;          // CL output [frame][H'][W'][OC]
     const float *inv_den = nullptr;    // [frame][OC]
@@ -93,6 +94,9 @@ struct ConvArgs {
 };
 
 int modconv_k_align(bool f16);
+// whether the conv reads A in chunk-major order (ConvArgs::A_chunk); a
+// function of the per-frame shape only
+bool modconv_uses_chunk_A(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
 bool modconv_fusable(int OC, int r, bool f16);
 // split-K factor of a conv (depends on the per-frame shape only)
