@@ -195,6 +195,47 @@ int tpmd_stage_conv_tail(tpmd_ctx *ctx, int j, const float *c1, int n, const flo
                          const float *s_flow, const float *flow_prev, const float *rgb_prev,
                          float *flow, float *trunk, float *rgb, float *warp, void *stream);
 
+/* ---- motion encoder ---------------------------------------------------- */
+
+/* tp::motion_enc (src/motion_enc.h:20-30, src/motion_enc.cpp:50-184): the
+ * LIA EncoderApp pyramid (EqualConv2d / FusedLeakyReLU / Blur ResBlocks,
+ * 512 -> 4), the 5-layer EqualLinear fc chain and the baked Direction Q.
+ * It runs once per portrait; its feats feed tpmd_set_feats_device. */
+typedef struct tpme_ctx tpme_ctx;
+
+/* device / ftype as tpmd_create (ftype "f16": tensors kept f16 are GEMM
+ * operands in f16, with the other operand rounded to f16, as ggml's
+ * im2col and vec_dot convert them).  n_blocks: 7 for the 512x512 encoder;
+ * ch_in / ch_out: NULL for the reference widths {32,64,128,256,512,512,512}
+ * / {64,128,256,512,512,512,512} (src/motion_enc.cpp:47-48), or per-ResBlock
+ * lists (multiples of 32, ch_in[i+1] == ch_out[i]) for reduced test models.
+ * The input image is (4 << n_blocks) pixels square.  NULL on failure. */
+tpme_ctx *tpme_create(int device, const char *ftype, int n_blocks, const int *ch_in, const int *ch_out);
+void tpme_destroy(tpme_ctx *ctx);
+const char *tpme_last_error(const tpme_ctx *ctx);
+/* the encoder tensors in GGUF names (enc.* and dec.direction.Q), i = 0.. ;
+ * NULL past the end */
+const char *tpme_weight_name(const tpme_ctx *ctx, int i, int64_t *n, int *is_matrix);
+/* as tpmd_set_weight: raw values in torch order, motion_ae_scale folded at
+ * load unless TPMD_W_FOLDED (src/motion_enc.cpp:14-45) */
+int tpme_set_weight(tpme_ctx *ctx, const char *name, const float *data, int64_t n, int flags);
+/* conv weights to tap-major GEMM operands, device upload; "missing tensor
+ * <name>" when one was not set */
+int tpme_prepare(tpme_ctx *ctx);
+/* motion_enc::run (src/motion_enc.cpp:50-184): image [3][R][R] f32 CHW in
+ * [-1,1] (host, or device when on_device != 0).  Synchronous. */
+int tpme_run(tpme_ctx *ctx, const float *image, int on_device);
+/* the last run's menc_result vectors (src/motion_enc.h:10-18), host copies:
+ * appearance [512], lambda [20], motion [512] = Q lambda; any may be NULL */
+int tpme_result(const tpme_ctx *ctx, float *appearance, float *lambda, float *motion);
+/* feats j of the last run: device [r*r][C] f32, r = 8 << j (= encoder level
+ * n_blocks - 1 - j), valid until the next run or destroy; pass all seven
+ * to tpmd_set_feats_device.  NULL on a bad index or before a run. */
+const float *tpme_feat(const tpme_ctx *ctx, int j, int *C, int *r);
+/* host copy of pyramid level l (menc.conv<l>, l = 0..n_blocks), CL
+ * [r*r][C] f32; returns the element count, or -1 (dst NULL: count only) */
+int64_t tpme_level(tpme_ctx *ctx, int level, float *dst);
+
 /* ---- op-level entry points (no context) ------------------------------- */
 
 /* GGML_OP_BILINEAR_GATHER (patches/ggml-tp-ops.patch:41-60, :104-111,

@@ -72,6 +72,7 @@ def lib():
             "orc_tanh": (None, [P, I64, P]),
             "orc_sigmoid": (None, [P, I64, P]),
             "orc_conv2d_direct": (None, [P, I, I, I, P, I, I, I, I, P]),
+            "orc_conv2d_s": (None, [P, I, I, I, P, I, I, I, I, I, P]),
             "orc_num_threads": (I, []),
             "orc_set_num_threads": (None, [I]),
         }
@@ -235,6 +236,18 @@ def conv2d_direct(x, w, pad):
     OH, OW = IH + 2 * pad - KH + 1, IW + 2 * pad - KW + 1
     y = np.empty((OC, OH, OW), np.float32)
     lib().orc_conv2d_direct(_p(x), IC, IH, IW, _p(w), OC, KH, KW, pad, _p(y))
+    return y
+
+
+def conv2d_s(x, w, stride, pad):
+    """strided cross-correlation: x (IC, H, W), w (OC, IC, KH, KW)."""
+    x, w = _f32(x), _f32(w)
+    IC, IH, IW = x.shape
+    OC, IC2, KH, KW = w.shape
+    assert IC == IC2
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    y = np.empty((OC, OH, OW), np.float32)
+    lib().orc_conv2d_s(_p(x), IC, IH, IW, _p(w), OC, KH, KW, stride, pad, _p(y))
     return y
 
 

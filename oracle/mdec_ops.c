@@ -388,6 +388,37 @@ void orc_conv2d_direct(const float *x, int IC, int IH, int IW, const float *w, i
     }
 }
 
+/* direct 2-D cross-correlation with stride s (dilation 1) on SP maps:
+ * x [IC][IH][IW], w [OC][IC][KH][KW] -> y [OC][OH][OW], OH = (IH + 2p - KH) / s + 1.
+ * The encoder's strided convs (src/motion_enc.cpp:89-96 via conv2d,
+ * src/ops_common.h:12-25).  f32 accumulation in order (ic, kh, kw).      */
+void orc_conv2d_s(const float *x, int IC, int IH, int IW, const float *w, int OC, int KH, int KW,
+                  int stride, int pad, float *y) {
+    const int OH = (IH + 2 * pad - KH) / stride + 1, OW = (IW + 2 * pad - KW) / stride + 1;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t t = 0; t < (int64_t) OC * OH; t++) {
+        const int o = (int) (t / OH), oy = (int) (t % OH);
+        float *yr = y + ((size_t) o * OH + oy) * OW;
+        for (int ox = 0; ox < OW; ox++) yr[ox] = 0.0f;
+        for (int i = 0; i < IC; i++) {
+            const float *xp = x + (size_t) i * IH * IW;
+            const float *wp = w + ((size_t) o * IC + i) * KH * KW;
+            for (int kh = 0; kh < KH; kh++) {
+                const int iy = oy * stride + kh - pad;
+                if (iy < 0 || iy >= IH) continue;
+                const float *xr = xp + (size_t) iy * IW;
+                for (int kw = 0; kw < KW; kw++) {
+                    const float wv = wp[kh * KW + kw];
+                    for (int ox = 0; ox < OW; ox++) {
+                        const int ix = ox * stride + kw - pad;
+                        if (ix >= 0 && ix < IW) yr[ox] += wv * xr[ix];
+                    }
+                }
+            }
+        }
+    }
+}
+
 int orc_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

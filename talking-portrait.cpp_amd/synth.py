@@ -165,6 +165,63 @@ def workload(name, n_frames, ftype="f32", ic=REF_IC, oc=REF_OC):
             feats(1002, oc, w["sigma"]))
 
 
+# ---- motion encoder (src/motion_enc.cpp:47-160)
+ENC_IN = (32, 64, 128, 256, 512, 512, 512)
+ENC_OUT = (64, 128, 256, 512, 512, 512, 512)
+
+
+def enc_tensor_shapes(cin=ENC_IN, cout=ENC_OUT, dim=STYLE_DIM, n_motion=20):
+    """(name, torch shape) of every encoder tensor (GGUF names), with the
+    decoder's dec.direction.Q the encoder also reads"""
+    b0 = "enc.net_app.convs"
+    v = [(f"{b0}.0.0.weight", (cin[0], 3, 1, 1)), (f"{b0}.0.1.bias", (cin[0],))]
+    for i in range(1, len(cin) + 1):
+        c, co, b = cin[i - 1], cout[i - 1], f"{b0}.{i}"
+        v += [(f"{b}.conv1.0.weight", (c, c, 3, 3)), (f"{b}.conv1.1.bias", (c,)),
+              (f"{b}.conv2.0.kernel", (4, 4)), (f"{b}.conv2.1.weight", (co, c, 3, 3)),
+              (f"{b}.conv2.2.bias", (co,)), (f"{b}.skip.0.kernel", (4, 4)),
+              (f"{b}.skip.1.weight", (co, c, 1, 1))]
+    v.append((f"{b0}.{len(cin) + 1}.weight", (dim, cout[-1], 4, 4)))
+    for i in range(5):
+        v += [(f"enc.fc.{i}.weight", (n_motion if i == 4 else dim, dim)),
+              (f"enc.fc.{i}.bias", (n_motion if i == 4 else dim,))]
+    v.append(("dec.direction.Q", (dim, n_motion)))
+    return v
+
+
+def enc_raw_weights(seed=1004, ftype="f32", cin=ENC_IN, cout=ENC_OUT):
+    """name -> (float32 array in torch shape, f16_in_file), seed 1004: every
+    .weight ~ N(0,1) (raw, before the Equal* folds), biases ~ N(0,1) * 0.1,
+    blur kernels [1,3,3,1] x [1,3,3,1] / 64 (downsampling Blur: no gain),
+    dec.direction.Q QR-orthonormal (512 x 20)."""
+    out = {}
+    for name, shape in enc_tensor_shapes(cin, cout):
+        g = _rng(seed, name)
+        if name.endswith(".kernel"):
+            a = (blur_kernel() / np.float32(4.0)).astype(np.float32)
+        elif name == "dec.direction.Q":
+            a = np.linalg.qr(g.standard_normal(shape))[0].astype(np.float32)
+        elif name.endswith(".weight"):
+            a = g.standard_normal(shape, dtype=np.float32)
+        else:
+            a = (g.standard_normal(shape, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+        f16 = ftype == "f16" and len(shape) >= 2 and not name.endswith(".kernel")
+        if f16:
+            a = a.astype(np.float16).astype(np.float32)
+        out[name] = (np.ascontiguousarray(a), f16)
+    return out
+
+
+def image(seed=1005, res=512):
+    """(3, res, res) float32 CHW in [-1, 1]: a smooth random field (a
+    periodic gaussian blur of N(0,1), sigma 4 px) scaled and clipped like a
+    normalised photograph"""
+    f = _rng(seed, "image").standard_normal((res, res, 3))
+    f = _blur_wrap(f, 4.0)
+    f = f / f.std() * 0.5
+    return np.ascontiguousarray(np.clip(f, -1.0, 1.0).transpose(2, 0, 1).astype(np.float32))
+
+
 def grid(n, lo, hi, seed=1003, jitter=0.0, res=None):
     """(n, 2) interleaved grid-sample coordinates ~ U(lo, hi) [+ U(-.5,.5)*jitter/res]."""
     g = _rng(seed, "grid")

@@ -78,6 +78,16 @@ def lib():
             "tpmd_gather_taps": (I, [P, I, I, I64, I, P, P, P, P, P]),
             "tpmd_upfirdn2x": (I, [P, P, P, I, I, I64, P]),
             "tpmd_flow_grid": (I, [P, P, P, I64, P]),
+            "tpme_create": (P, [I, C, I, P, P]),
+            "tpme_destroy": (None, [P]),
+            "tpme_last_error": (C, [P]),
+            "tpme_weight_name": (C, [P, I, P, P]),
+            "tpme_set_weight": (I, [P, C, P, I64, I]),
+            "tpme_prepare": (I, [P]),
+            "tpme_run": (I, [P, P, I]),
+            "tpme_result": (I, [P, P, P, P]),
+            "tpme_feat": (P, [P, I, P, P]),
+            "tpme_level": (I64, [P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -90,7 +100,7 @@ def lib():
 def header_symbols():
     """Function names declared in include/tpmd.h."""
     txt = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(tpmd_[a-z0-9_]+)\s*\(", txt)))
+    return sorted(set(re.findall(r"\b(tpm[de]_[a-z0-9_]+)\s*\(", txt)))
 
 
 def _ptr(t):
@@ -200,7 +210,8 @@ class MotionDecoder:
         self._check(lib().tpmd_set_feats(self.h, ctypes.cast(ptrs, ctypes.c_void_p)))
 
     def set_feats_device(self, feats):
-        ptrs = (ctypes.c_void_p * len(feats))(*[f.data_ptr() for f in feats])
+        """feats: torch cuda tensors, or raw device addresses (MotionEncoder.feats_device)"""
+        ptrs = (ctypes.c_void_p * len(feats))(*[f if isinstance(f, int) else f.data_ptr() for f in feats])
         self._check(lib().tpmd_set_feats_device(self.h, ctypes.cast(ptrs, ctypes.c_void_p)))
 
     # ---- decode
@@ -354,3 +365,99 @@ def flow_grid(fl, xs, stream=None):
     if rc != 0:
         raise TpmdError("tpmd_flow_grid: invalid arguments")
     return y
+
+
+class MotionEncoder:
+    """tp::motion_enc (src/motion_enc.h:20-30) over tpme_*: run an image,
+    read appearance / lambda / motion and the decoder feats.
+
+        enc = MotionEncoder("f16"); enc.set_weights(raw); enc.prepare()
+        out = enc.run(image)                 # dict of numpy arrays
+        dec.set_feats_device(enc.feats_device())
+    """
+
+    def __init__(self, ftype="f32", ch_in=None, ch_out=None, device=0):
+        L = lib()
+        self.ftype = ftype
+        nb = 7 if ch_in is None else len(ch_in)
+        self.ch_in = tuple(ch_in) if ch_in is not None else (32, 64, 128, 256, 512, 512, 512)
+        self.ch_out = tuple(ch_out) if ch_out is not None else (64, 128, 256, 512, 512, 512, 512)
+        self.n_blocks = nb
+        a = (ctypes.c_int * nb)(*self.ch_in) if ch_in is not None else None
+        b = (ctypes.c_int * nb)(*self.ch_out) if ch_out is not None else None
+        h = L.tpme_create(device, ftype.encode(), nb, a, b)
+        if not h:
+            raise TpmdError("tpme_create failed")
+        self.h = h
+        self.res = 4 << nb
+
+    def _check(self, rc):
+        if rc < 0:
+            raise TpmdError(lib().tpme_last_error(self.h).decode())
+        return rc
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().tpme_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weight_names(self):
+        out, i = [], 0
+        n = ctypes.c_int64()
+        while True:
+            nm = lib().tpme_weight_name(self.h, i, ctypes.byref(n), None)
+            if nm is None:
+                return out
+            out.append((nm.decode(), n.value))
+            i += 1
+
+    def set_weights(self, raw, folded=False):
+        """raw: name -> (array in torch shape, f16_in_file)"""
+        for name, _ in self.weight_names():
+            arr, f16 = raw[name]
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            flags = (W_F16_FILE if f16 else 0) | (W_FOLDED if folded else 0)
+            self._check(lib().tpme_set_weight(self.h, name.encode(), _hptr(a), a.size, flags))
+
+    def prepare(self):
+        self._check(lib().tpme_prepare(self.h))
+
+    def run(self, image):
+        """image (3, R, R) f32 numpy (host) or torch cuda tensor -> dict with
+        appearance, lambda, motion and feats (list of (r*r, C) numpy)"""
+        if hasattr(image, "is_cuda") and image.is_cuda:
+            self._check(lib().tpme_run(self.h, _ptr(image), 1))
+        else:
+            im = np.ascontiguousarray(image, dtype=np.float32)
+            assert im.shape == (3, self.res, self.res)
+            self._check(lib().tpme_run(self.h, _hptr(im), 0))
+        app = np.empty(512, np.float32)
+        lam = np.empty(20, np.float32)
+        mot = np.empty(512, np.float32)
+        self._check(lib().tpme_result(self.h, _hptr(app), _hptr(lam), _hptr(mot)))
+        return {"appearance": app, "lambda": lam, "motion": mot,
+                "feats": [self.level(self.n_blocks - 1 - j) for j in range(self.n_blocks)]}
+
+    def level(self, l):
+        """pyramid level l (menc.conv<l>) as (r*r, C) numpy"""
+        n = self._check(lib().tpme_level(self.h, l, None))
+        out = np.empty(n, np.float32)
+        self._check(lib().tpme_level(self.h, l, _hptr(out)))
+        r = self.res >> l
+        return out.reshape(r * r, -1)
+
+    def feats_device(self):
+        """device pointers of the last run's feats j = 0 .. n_blocks-1"""
+        ptrs = []
+        for j in range(self.n_blocks):
+            p = lib().tpme_feat(self.h, j, None, None)
+            if not p:
+                raise TpmdError("encoder has not run")
+            ptrs.append(p)
+        return ptrs

@@ -22,6 +22,13 @@ def om():
 
 
 @pytest.fixture(scope="session")
+def oracle_menc():
+    from oracle import mdec, menc
+    mdec.lib()
+    return menc
+
+
+@pytest.fixture(scope="session")
 def torch_cuda():
     import torch
     if not torch.cuda.is_available():

@@ -108,3 +108,38 @@ def decode(raw, latent, feats, ic, oc, n_stages=None, taps=None):
             taps[f"r{r}.rgb"] = rgb[0].numpy()
         out = trunk
     return skip[0].numpy()
+
+
+def encode(raw, image, cin, cout, taps=None):
+    """Upstream LIA EncoderApp + fc chain + Direction (EqualConv2d runtime
+    scales, FusedLeakyReLU x sqrt2, ResBlock (conv2 + skip) / sqrt2, Blur as
+    upfirdn2d with the normalised [1,3,3,1] kernel), float64, NO folds.
+    raw: name -> (array, _) raw synthetic encoder weights; image (3, H, W).
+    Returns (appearance, lambda, motion, pyramid list conv0..conv7) numpy."""
+    dt = torch.float64
+    T = {k: torch.tensor(v[0], dtype=dt) for k, v in raw.items()}
+
+    def eqconv(x, W, stride, pad):
+        fan_in = W.shape[1] * W.shape[2] * W.shape[3]
+        return F.conv2d(x, W * (1.0 / math.sqrt(fan_in)), stride=stride, padding=pad)
+
+    b0 = "enc.net_app.convs"
+    x = torch.tensor(image, dtype=dt)[None]
+    x = fused_lrelu(eqconv(x, T[f"{b0}.0.0.weight"], 1, 0), T[f"{b0}.0.1.bias"])
+    pyr = [x]
+    for i in range(1, len(cin) + 1):
+        b = f"{b0}.{i}"
+        out = fused_lrelu(eqconv(x, T[f"{b}.conv1.0.weight"], 1, 1), T[f"{b}.conv1.1.bias"])
+        out = upfirdn2d(out, T[f"{b}.conv2.0.kernel"], pad=(2, 2))
+        out = fused_lrelu(eqconv(out, T[f"{b}.conv2.1.weight"], 2, 0), T[f"{b}.conv2.2.bias"])
+        skip = eqconv(upfirdn2d(x, T[f"{b}.skip.0.kernel"], pad=(1, 1)), T[f"{b}.skip.1.weight"], 2, 0)
+        x = (out + skip) / SQRT2
+        pyr.append(x)
+    app = eqconv(x, T[f"{b0}.{len(cin) + 1}.weight"], 1, 0).reshape(-1)
+    h = app
+    for i in range(5):
+        h = equal_linear(h[None], T[f"enc.fc.{i}.weight"], T[f"enc.fc.{i}.bias"])[0]
+        if taps is not None:
+            taps[f"menc.fc{i}"] = h.numpy()
+    motion = T["dec.direction.Q"] @ h
+    return app.numpy(), h.numpy(), motion.numpy(), [p[0].numpy() for p in pyr]
