@@ -107,6 +107,50 @@ def roofline(name, flops, nbytes, us, ftype):
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4)}
 
 
+def encoder_flops(cin, cout, res=512, dim=512):
+    """algorithmic FLOPs of one motion-encoder run (conv MACs x 2: stem,
+    per ResBlock conv1 3x3, conv2 3x3 stride 2, skip 1x1 stride 2, the final
+    4x4 conv, the fc chain and Q)"""
+    f = 2 * res * res * 3 * cin[0]
+    r = res
+    for c, co in zip(cin, cout):
+        f += 2 * r * r * 9 * c * c + 2 * (r // 2) ** 2 * (9 + 1) * c * co
+        r //= 2
+    f += 2 * dim * 16 * cout[-1] + 2 * (4 * dim * dim + 20 * dim) + 2 * dim * 20
+    return f
+
+
+def encoder_timing(ftype, reps=20):
+    """the motion encoder (once per portrait) on the synthetic image, device
+    resident, synchronous runs: median ms and MFMA fraction"""
+    import numpy as np
+    import torch
+    import synth
+    import tpmd
+    enc = tpmd.MotionEncoder(ftype)
+    enc.set_weights(synth.enc_raw_weights(1004, ftype))
+    enc.prepare()
+    img = torch.from_numpy(synth.image(1005)).cuda()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        enc.run(img)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        lib = tpmd.lib()
+        if lib.tpme_run(enc.h, tpmd._ptr(img), 1) < 0:
+            raise tpmd.TpmdError(lib.tpme_last_error(enc.h).decode())
+        ts.append(time.perf_counter() - t0)
+    ms = float(np.median(ts)) * 1e3
+    fl = encoder_flops(enc.ch_in, enc.ch_out)
+    peak = 2500.0 if ftype == "f16" else 157.3
+    enc.close()
+    return {"ms_per_portrait": round(ms, 3), "gflop": round(fl / 1e9, 2),
+            "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / peak, 4),
+            "note": "tpme_run, 512x512 image resident in HBM, synchronous (host clock)"}
+
+
 def cpu_baseline(ftype_unused=None):
     """the CPU oracle's fast graph (f32, numpy/OpenBLAS + OpenMP C ops) on
     this host, one 512x512 frame"""
@@ -229,6 +273,7 @@ def main():
         host[name] = round(n_seq / (time.perf_counter() - t0h), 1)
     out["host_delivered_fps"] = {"frames": n_seq, **host,
                                  "note": "pageable host buffer, PCIe download included"}
+    out["encoder"] = encoder_timing(args.ftype)
     if args.copy_probe:
         copy_probe()
     if not args.no_cpu_baseline:

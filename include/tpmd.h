@@ -219,6 +219,11 @@ const char *tpme_weight_name(const tpme_ctx *ctx, int i, int64_t *n, int *is_mat
 /* as tpmd_set_weight: raw values in torch order, motion_ae_scale folded at
  * load unless TPMD_W_FOLDED (src/motion_enc.cpp:14-45) */
 int tpme_set_weight(tpme_ctx *ctx, const char *name, const float *data, int64_t n, int flags);
+/* weights_t::load for the encoder's tensors (src/gguf_load.cpp:51-197), as
+ * tpmd_load_gguf: every enc.* tensor and dec.direction.Q of a
+ * "float-motion-ae" GGUF v3 file through tpme_set_weight (F16 tensors with
+ * TPMD_W_F16_FILE); 0, or -1 with the reason in err[0..err_size) */
+int tpme_load_gguf(tpme_ctx *ctx, const char *path, char *err, size_t err_size);
 /* conv weights to tap-major GEMM operands, device upload; "missing tensor
  * <name>" when one was not set */
 int tpme_prepare(tpme_ctx *ctx);

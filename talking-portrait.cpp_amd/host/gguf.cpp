@@ -1,5 +1,5 @@
 // GGUF v3 reader (see gguf.h) and the C entry points tpmd_load_gguf /
-// tpmd_gguf_read_tensor of include/tpmd.h.
+// tpme_load_gguf / tpmd_gguf_read_tensor of include/tpmd.h.
 #include "gguf.h"
 
 #include <cstdio>
@@ -233,6 +233,32 @@ int tpmd_load_gguf(tpmd_ctx *ctx, const char *path, char *err, size_t err_size) 
                         " elements, expected " + std::to_string(n));
         if (tpmd_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
             return fail(tpmd_last_error(ctx));
+    }
+    return 0;
+}
+
+int tpme_load_gguf(tpme_ctx *ctx, const char *path, char *err, size_t err_size) {
+    auto fail = [&](const std::string &m) {
+        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
+        return -1;
+    };
+    if (!ctx || !path) return fail("tpme_load_gguf: null context or path");
+    tp::gguf_file f;
+    std::string e;
+    if (!f.open(path, "float-motion-ae", e)) return fail(e);
+    std::vector<float> v;
+    for (int i = 0;; i++) {
+        int64_t n = 0;
+        const char *name = tpme_weight_name(ctx, i, &n, nullptr);
+        if (!name) break;
+        if (!f.find(name)) continue;  // prepare() names the first missing tensor
+        bool f16 = false;
+        if (!f.read(name, v, f16, e)) return fail(e);
+        if ((int64_t) v.size() != n)
+            return fail(std::string(path) + ": tensor " + name + " has " + std::to_string(v.size()) +
+                        " elements, expected " + std::to_string(n));
+        if (tpme_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
+            return fail(tpme_last_error(ctx));
     }
     return 0;
 }

@@ -88,6 +88,7 @@ def lib():
             "tpme_result": (I, [P, P, P, P]),
             "tpme_feat": (P, [P, I, P, P]),
             "tpme_level": (I64, [P, I, P]),
+            "tpme_load_gguf": (I, [P, C, P, ctypes.c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -424,6 +425,12 @@ class MotionEncoder:
             a = np.ascontiguousarray(arr, dtype=np.float32)
             flags = (W_F16_FILE if f16 else 0) | (W_FOLDED if folded else 0)
             self._check(lib().tpme_set_weight(self.h, name.encode(), _hptr(a), a.size, flags))
+
+    def load_gguf(self, path):
+        """every encoder tensor of a motion_ae GGUF file (tpme_load_gguf)"""
+        err = ctypes.create_string_buffer(512)
+        if lib().tpme_load_gguf(self.h, str(path).encode(), err, len(err)) < 0:
+            raise TpmdError(err.value.decode())
 
     def prepare(self):
         self._check(lib().tpme_prepare(self.h))

@@ -6,6 +6,7 @@ the decoder exactly as the same feats uploaded from the host do."""
 import numpy as np
 import pytest
 
+import gguf_writer
 import synth
 import tpmd
 from metrics import cosine, rel_l2
@@ -90,3 +91,26 @@ def test_encoder_error_contract(torch_cuda):
     z = np.zeros(1, np.float32)
     assert tpmd.lib().tpme_set_weight(enc.h, b"enc.nope", z.ctypes.data, 1, 0) == -1
     assert b"unknown encoder tensor enc.nope" in tpmd.lib().tpme_last_error(enc.h)
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_encoder_from_gguf(torch_cuda, tmp_path, ftype):
+    """tpme_load_gguf on a motion_ae file holding the encoder tensors gives
+    the encoder of the same named weights, bit for bit"""
+    raw = synth.enc_raw_weights(1004, ftype, SMALL_IN, SMALL_OUT)
+    path = tmp_path / f"motion_ae_enc_{ftype}.gguf"
+    gguf_writer.write(path, {k: (v, f16) for k, (v, f16) in raw.items()}, f16=ftype == "f16")
+    img = synth.image(1005)
+    outs = []
+    for use_file in (False, True):
+        enc = tpmd.MotionEncoder(ftype, SMALL_IN, SMALL_OUT)
+        if use_file:
+            enc.load_gguf(path)
+        else:
+            enc.set_weights(raw)
+        enc.prepare()
+        outs.append(enc.run(img))
+    for k in ("appearance", "lambda", "motion"):
+        assert np.array_equal(outs[0][k], outs[1][k]), k
+    for a, b in zip(outs[0]["feats"], outs[1]["feats"]):
+        assert np.array_equal(a, b)
