@@ -12,11 +12,14 @@
 // Output file: f32 frames [n_frames][3][R][R], then the single-frame decode
 // of frame 0 [3][R][R].  Exit status 0 on success; errors on stderr.
 //
-//   shim_check <blob> <out> [device] [gguf]
+//   shim_check <blob> <out> [device] [gguf] [image]
 //
 // With a GGUF path the weights come from that checkpoint through
 // tp::gguf_weight_source (the reference's tp_load flow, src/tp.cpp:13-41)
-// and the blob's weight section is ignored.
+// and the blob's weight section is ignored.  With an image file too (f32
+// [3][512][512] CHW), tp::motion_enc runs on it and its menc_result replaces
+// the blob's feats (the generation flow, src/pipeline.cpp:113-115); the
+// output then ends with appearance [512], lambda [20] and motion [512].
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -26,6 +29,7 @@
 
 #include "gguf.h"
 #include "motion_dec.h"
+#include "motion_enc.h"
 
 namespace {
 
@@ -79,7 +83,7 @@ struct no_taps {
 
 int main(int argc, char **argv) {
     if (argc < 3) {
-        fprintf(stderr, "usage: shim_check <blob> <out> [device] [gguf]\n");
+        fprintf(stderr, "usage: shim_check <blob> <out> [device] [gguf] [image]\n");
         return 2;
     }
     reader r;
@@ -147,7 +151,26 @@ int main(int argc, char **argv) {
         gw.f = &gf;
         dec.w = &gw;
     }
-    if (!dec.prepare(be, err) || !dec.build(be, false, err) || !dec.set_feats(m, err)) {
+    tp::menc_result mr;
+    const bool with_enc = argc > 5;
+    if (with_enc) {
+        std::vector<float> img((size_t) 3 * 512 * 512);
+        FILE *fi = fopen(argv[5], "rb");
+        if (!fi || fread(img.data(), 4, img.size(), fi) != img.size()) {
+            fprintf(stderr, "cannot read image %s\n", argv[5]);
+            return 1;
+        }
+        fclose(fi);
+        tp::motion_enc enc;
+        enc.w = dec.w;
+        no_taps et;
+        if (!enc.run(be, img.data(), mr, et, err)) {
+            fprintf(stderr, "shim_check: %s\n", err.c_str());
+            return 1;
+        }
+    }
+    if (!dec.prepare(be, err) || !dec.build(be, false, err) ||
+        !(with_enc ? dec.set_feats(mr, err) : dec.set_feats(m, err))) {
         fprintf(stderr, "shim_check: %s\n", err.c_str());
         return 1;
     }
@@ -170,6 +193,11 @@ int main(int argc, char **argv) {
     if (!dec.decode(be, styles.data(), out.data() + (size_t) nf * fsz, tap, err)) {
         fprintf(stderr, "shim_check: %s\n", err.c_str());
         return 1;
+    }
+    if (with_enc) {
+        out.insert(out.end(), mr.appearance.begin(), mr.appearance.end());
+        out.insert(out.end(), mr.lambda.begin(), mr.lambda.end());
+        out.insert(out.end(), mr.motion.begin(), mr.motion.end());
     }
     FILE *f = fopen(argv[2], "wb");
     if (!f || fwrite(out.data(), 4, out.size(), f) != out.size()) {

@@ -68,3 +68,45 @@ def test_shim_errors(torch_cuda, tmp_path):
     p = subprocess.run([SHIM, str(blob), str(tmp_path / "o")], capture_output=True, text=True,
                        timeout=120)
     assert p.returncode == 1 and "missing tensor dec.to_rgbs.3.bias" in p.stderr
+
+
+def test_shim_encoder_to_decoder(torch_cuda, tmp_path):
+    """the generation flow through both C++ shims, weights from one motion_ae
+    GGUF holding enc.* and dec.*: tp::motion_enc::run on an image, its
+    menc_result into tp::motion_dec::set_feats, then decode_batch — equal,
+    bit for bit, to MotionEncoder + MotionDecoder through the binding"""
+    import gguf_writer
+    ftype = "f16"
+    raw, lat, feats = synth.workload("smooth", 3, ftype, IC, OC)
+    # the encoder channel plan that produces feats with OC[j] channels
+    cout = tuple(OC[5 - i] for i in range(6)) + (OC[0],)
+    cin = (OC[6],) + cout[:6]
+    raw_e = synth.enc_raw_weights(1004, ftype, cin, cout)
+    gguf = tmp_path / "motion_ae.gguf"
+    gguf_writer.write(gguf, {**raw, **raw_e}, f16=True)
+    img = synth.image(1005)
+    img_path = tmp_path / "image.f32"
+    img.tofile(img_path)
+    blob, out = tmp_path / "in.blob", tmp_path / "out.f32"
+    write_blob(blob, raw, feats, lat, IC, OC, True)
+    env = dict(os.environ, TP_MDEC_BATCH="2")
+    p = subprocess.run([SHIM, str(blob), str(out), "0", str(gguf), str(img_path)], env=env,
+                       capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    R = 512
+    got = np.fromfile(out, np.float32)
+    frames = got[:4 * 3 * R * R].reshape(4, 3, R, R)
+    app, lam, mot = np.split(got[4 * 3 * R * R:], [512, 532])
+    enc = tpmd.MotionEncoder(ftype, cin, cout)
+    enc.set_weights(raw_e)
+    enc.prepare()
+    r = enc.run(img)
+    assert np.array_equal(app, r["appearance"]) and np.array_equal(lam, r["lambda"])
+    assert np.array_equal(mot, r["motion"])
+    dec = tpmd.MotionDecoder(ftype, len(IC), IC, OC)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(2)
+    dec.set_feats(r["feats"])
+    want = np.concatenate([dec.decode_batch(lat[t:t + 2]) for t in range(0, 3, 2)])
+    assert np.array_equal(frames[:3], want)
