@@ -241,6 +241,50 @@ const float *tpme_feat(const tpme_ctx *ctx, int j, int *C, int *r);
  * [r*r][C] f32; returns the element count, or -1 (dst NULL: count only) */
 int64_t tpme_level(tpme_ctx *ctx, int level, float *dst);
 
+/* ---- flow-matching transformer ------------------------------------------ */
+
+/* tp::fmt_model (src/fmt.h:9-36, src/fmt.cpp): 8 DiT blocks with per-frame
+ * adaLN modulation and a banded attention mask, CFG-batched over the three
+ * condition branches [uncond, full, audio_only]; and its ODE chunk sampler
+ * (sample_chunk, src/pipeline.cpp:12-91). */
+typedef struct tpfm_ctx tpfm_ctx;
+/* fmt_model's hyper-parameters; defaults as src/fmt.h:10-16 */
+typedef struct tpfm_config {
+    int dim_h, depth, n_heads, dim_w, dim_a, dim_e;
+    int chunk_frames, prev_frames, attn_window, t_freq_dim, nfe;
+    float mlp_ratio, ln_eps, a_cfg, e_cfg, r_cfg;
+} tpfm_config;
+void tpfm_default_config(tpfm_config *cfg);
+/* the float.fmt.* keys of a "float-fmt" GGUF file (src/fmt.cpp:8-26) over
+ * the defaults; 0, or -1 with the reason in err */
+int tpfm_read_config(const char *gguf_path, tpfm_config *cfg, char *err, size_t err_size);
+/* ftype as tpmd_create.  Constraints of this build: dim_h % n_heads == 0,
+ * head dim <= 256, attn_window <= 7, and dim_h, dim_w, t_freq_dim and the
+ * MLP width multiples of 32.  NULL on failure (message on stderr). */
+tpfm_ctx *tpfm_create(int device, const char *ftype, const tpfm_config *cfg);
+void tpfm_destroy(tpfm_ctx *ctx);
+const char *tpfm_last_error(const tpfm_ctx *ctx);
+/* the FMT tensors (GGUF names), i = 0.. ; NULL past the end */
+const char *tpfm_weight_name(const tpfm_ctx *ctx, int i, int64_t *n, int *is_matrix);
+/* values as stored (no load-time folds for the FMT); TPMD_W_F16_FILE as
+ * tpmd_set_weight (the f16 keep rule of src/gguf_load.cpp:149-153) */
+int tpfm_set_weight(tpfm_ctx *ctx, const char *name, const float *data, int64_t n, int flags);
+/* every FMT tensor of a "float-fmt" GGUF v3 file; 0 or -1 with err */
+int tpfm_load_gguf(tpfm_ctx *ctx, const char *path, char *err, size_t err_size);
+/* device upload; "missing tensor <name>" when one was not set */
+int tpfm_prepare(tpfm_ctx *ctx);
+/* fmt_model::forward (src/fmt.h:27-31): x60 [total][dim_w], cond
+ * [3][total][dim_w+dim_a+dim_e], flow time t -> v_out [3][total][dim_w];
+ * host buffers, synchronous */
+int tpfm_forward(tpfm_ctx *ctx, const float *x60, const float *cond, float t, float *v_out);
+/* sample_chunk (src/pipeline.cpp:12-91): the CFG condition rows from wr
+ * [dim_w], prev_wa [prev][dim_a], cond_audio [chunk][dim_a] and emotion
+ * (-1: none), then nfe - 1 Euler steps of the CFG-combined velocity from x0
+ * [chunk][dim_w] with prev_x [prev][dim_w] -> motion_out [chunk][dim_w];
+ * host buffers, synchronous */
+int tpfm_sample_chunk(tpfm_ctx *ctx, const float *wr, const float *prev_x, const float *prev_wa,
+                      const float *cond_audio, int emotion, const float *x0, float *motion_out);
+
 /* ---- op-level entry points (no context) ------------------------------- */
 
 /* GGML_OP_BILINEAR_GATHER (patches/ggml-tp-ops.patch:41-60, :104-111,

@@ -15,6 +15,11 @@
 
 namespace tpmd {
 
+// tanh-approximated GELU (ggml_gelu's formula): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+__device__ __forceinline__ float gelu_tanh(float x) {
+    return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+}
+
 template <typename T> __device__ __forceinline__ T enc_cast(float v);
 template <> __device__ __forceinline__ float enc_cast<float>(float v) { return v; }
 template <> __device__ __forceinline__ half_t enc_cast<half_t>(float v) { return (half_t) v; }
@@ -161,16 +166,18 @@ __global__ __launch_bounds__(256) void enc_conv_kernel(EncConvParams p) {
         for (int j = 0; j < 4; j++) {
             float a = acc[i * 4 + j];
             if (p.bias) a = a + p.bias[o + j];
-            if (p.leaky) a = leaky(a);
+            if (p.leaky == 1) a = leaky(a);
+            else if (p.leaky == 2) a = gelu_tanh(a);
+            if (p.gate) a = p.gate[(int64_t) n * p.gstride + o + j] * a;
             v[j] = a;
         }
         const int64_t off = (int64_t) n * OC + o;
         if (p.res) {
             const floatx4 r = *(const floatx4 *) (p.res + off);
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = v[j] + r[j];
+            for (int j = 0; j < 4; j++) v[j] = r[j] + v[j];
         }
-        *(floatx4 *) (p.Y + off) = floatx4{v[0], v[1], v[2], v[3]};
+        if (p.Y) *(floatx4 *) (p.Y + off) = floatx4{v[0], v[1], v[2], v[3]};
         if (p.Ya) {
             if (p.ya_f16) store4<half_t>((half_t *) p.Ya + off, v[0], v[1], v[2], v[3]);
             else store4<float>((float *) p.Ya + off, v[0], v[1], v[2], v[3]);

@@ -1,0 +1,236 @@
+// Flow-matching transformer pieces (src/fmt.cpp:44-205, src/pipeline.cpp:38-91)
+// around the MFMA GEMM of k_enc.hip (a linear layer is its 1x1 conv over a
+// row of tokens):
+//
+//   fmt_convert_kernel   f32 rows -> GEMM operand type, zero-padding K
+//   fmt_silu_kernel      in place, the t-embedder's hidden layer
+//   fmt_cond_kernel      silu(c_embed + t_embed) in the adaLN GEMMs' operand type
+//   fmt_xpos_kernel      x = x_embed + pos, replicated over the CFG branches
+//   fmt_ln_mod_kernel    LayerNorm (no affine) then adaLN modulate: n*scale + n + shift
+//   fmt_attn_kernel      banded multi-head attention (softmax(q k / sqrt(hd) + mask) v)
+//   fmt_euler_kernel     CFG combination of the three branches and the Euler step
+#include "tpmd_conv.h"
+#include "tpmd_fmt.h"
+
+namespace tpmd {
+
+template <typename T> __device__ __forceinline__ T fmt_cast(float v);
+template <> __device__ __forceinline__ float fmt_cast<float>(float v) { return v; }
+template <> __device__ __forceinline__ half_t fmt_cast<half_t>(float v) { return (half_t) v; }
+
+__device__ __forceinline__ float fmt_silu(float x) { return x / (1.0f + expf(-x)); }
+
+template <typename TO>
+__global__ __launch_bounds__(256) void fmt_convert_kernel(const float *__restrict__ x, int rows, int cols, int ld,
+                                                          TO *__restrict__ y) {
+    const int64_t total = (int64_t) rows * ld;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        const int64_t r = i / ld;
+        const int c = (int) (i - r * ld);
+        y[i] = fmt_cast<TO>(c < cols ? x[r * cols + c] : 0.0f);
+    }
+}
+
+__global__ __launch_bounds__(256) void fmt_silu_kernel(float *__restrict__ x, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = fmt_silu(x[i]);
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256) void fmt_cond_kernel(const float *__restrict__ clin, const float *__restrict__ temb,
+                                                       int rows, int H, TO *__restrict__ y) {
+    const int64_t total = (int64_t) rows * H;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        const int c = (int) (i % H);
+        y[i] = fmt_cast<TO>(fmt_silu(clin[i] + temb[c]));
+    }
+}
+
+__global__ __launch_bounds__(256) void fmt_xpos_kernel(const float *__restrict__ x1, const float *__restrict__ pos,
+                                                       int T, int H, int B, float *__restrict__ x) {
+    const int64_t per = (int64_t) T * H, total = per * B;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        const int64_t j = i % per;
+        x[i] = x1[j] + pos[j];
+    }
+}
+
+// one workgroup per row of H: mean, then the variance of the centred values
+// (two passes over registers), n = (x - mean) / sqrt(var + eps),
+// h = n * scale + n + shift
+template <typename TO>
+__global__ __launch_bounds__(256) void fmt_ln_mod_kernel(const float *__restrict__ x, const float *__restrict__ mod,
+                                                         int64_t mstride, int shift_off, int scale_off, int H,
+                                                         float eps, TO *__restrict__ y) {
+    constexpr int MAXV = 16;  // H <= 4096
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const float *xr = x + (int64_t) row * H;
+    float v[MAXV];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXV; k++) {
+        const int i = tid + k * 256;
+        v[k] = i < H ? xr[i] : 0.0f;
+        s += v[k];
+    }
+    auto block_sum = [&](float a) {
+        a = group_sum<64>(a);
+        __syncthreads();
+        if (lane == 0) red[wid] = a;
+        __syncthreads();
+        return red[0] + red[1] + red[2] + red[3];
+    };
+    const float mean = block_sum(s) / (float) H;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXV; k++) {
+        const int i = tid + k * 256;
+        if (i < H) {
+            v[k] = v[k] - mean;
+            s2 += v[k] * v[k];
+        }
+    }
+    const float var = block_sum(s2) / (float) H;
+    const float inv = 1.0f / sqrtf(var + eps);
+    const float *mr = mod + (int64_t) row * mstride;
+    TO *yr = y + (int64_t) row * H;
+#pragma unroll
+    for (int k = 0; k < MAXV; k++) {
+        const int i = tid + k * 256;
+        if (i < H) {
+            const float n = v[k] * inv;
+            yr[i] = fmt_cast<TO>((n * mr[scale_off + i] + n) + mr[shift_off + i]);
+        }
+    }
+}
+
+// one wave per (branch, head, query): the keys |tq - tk| <= w only (the
+// band mask's -inf elsewhere contributes exp(-inf) = 0), lanes over the
+// head dimension
+template <typename TO>
+__global__ __launch_bounds__(256) void fmt_attn_kernel(const float *__restrict__ qkv, int B, int T, int H, int nh,
+                                                       int w, float scale, TO *__restrict__ o) {
+    constexpr int MAXK = 15, MAXD = 4;  // 2w + 1 keys, head dim <= 256
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= B * nh * T) return;  // whole wave
+    const int tq = g % T, hh = (g / T) % nh, b = g / (T * nh);
+    const int hd = H / nh;
+    const int64_t rs = 3 * (int64_t) H;
+    const float *qr = qkv + ((int64_t) b * T + tq) * rs + hh * hd;
+    float q[MAXD];
+#pragma unroll
+    for (int k = 0; k < MAXD; k++) q[k] = lane + 64 * k < hd ? qr[lane + 64 * k] : 0.0f;
+    const int k0 = tq - w > 0 ? tq - w : 0, k1 = tq + w < T - 1 ? tq + w : T - 1;
+    float sc[MAXK];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MAXK; j++) {
+        sc[j] = -INFINITY;
+        const int tk = k0 + j;
+        if (tk <= k1) {
+            const float *kr = qkv + ((int64_t) b * T + tk) * rs + H + hh * hd;
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MAXD; k++)
+                if (lane + 64 * k < hd) a = __builtin_fmaf(q[k], kr[lane + 64 * k], a);
+            sc[j] = group_sum<64>(a) * scale;
+            mx = sc[j] > mx ? sc[j] : mx;
+        }
+    }
+    float den = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXK; j++) {
+        sc[j] = k0 + j <= k1 ? expf(sc[j] - mx) : 0.0f;
+        den += sc[j];
+    }
+    float acc[MAXD] = {};
+#pragma unroll
+    for (int j = 0; j < MAXK; j++) {
+        const int tk = k0 + j;
+        if (tk <= k1) {
+            const float *vr = qkv + ((int64_t) b * T + tk) * rs + 2 * H + hh * hd;
+#pragma unroll
+            for (int k = 0; k < MAXD; k++)
+                if (lane + 64 * k < hd) acc[k] = __builtin_fmaf(sc[j], vr[lane + 64 * k], acc[k]);
+        }
+    }
+    TO *orow = o + ((int64_t) b * T + tq) * H + hh * hd;
+#pragma unroll
+    for (int k = 0; k < MAXD; k++)
+        if (lane + 64 * k < hd) orow[lane + 64 * k] = fmt_cast<TO>(acc[k] / den);
+}
+
+// vc = (u + a_cfg (a - u)) + e_cfg (fu - a) for the chunk's rows, x += dt vc
+__global__ __launch_bounds__(256) void fmt_euler_kernel(const float *__restrict__ v, float *__restrict__ x60, int T,
+                                                        int P, int D, float a_cfg, float e_cfg, float dt) {
+    const int64_t n = (int64_t) (T - P) * D;
+    const int64_t per = (int64_t) T * D;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t) gridDim.x * 256) {
+        const int64_t j = (int64_t) P * D + i;
+        const float u = v[j], fu = v[per + j], a = v[2 * per + j];
+        const float vc = (u + a_cfg * (a - u)) + e_cfg * (fu - a);
+        x60[j] = x60[j] + dt * vc;
+    }
+}
+
+static unsigned fmt_grid(int64_t total) {
+    int64_t nb = (total + 255) / 256;
+    if (nb > 65536) nb = 65536;
+    return (unsigned) (nb < 1 ? 1 : nb);
+}
+
+hipError_t launch_fmt_convert(const float *x, int rows, int cols, int ld, void *y, bool f16, hipStream_t st) {
+    const unsigned g = fmt_grid((int64_t) rows * ld);
+    if (f16) hipLaunchKernelGGL(fmt_convert_kernel<half_t>, dim3(g), dim3(256), 0, st, x, rows, cols, ld, (half_t *) y);
+    else hipLaunchKernelGGL(fmt_convert_kernel<float>, dim3(g), dim3(256), 0, st, x, rows, cols, ld, (float *) y);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_silu(float *x, int n, hipStream_t st) {
+    hipLaunchKernelGGL(fmt_silu_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_cond(const float *clin, const float *temb, int rows, int H, void *y, bool f16, hipStream_t st) {
+    const unsigned g = fmt_grid((int64_t) rows * H);
+    if (f16) hipLaunchKernelGGL(fmt_cond_kernel<half_t>, dim3(g), dim3(256), 0, st, clin, temb, rows, H, (half_t *) y);
+    else hipLaunchKernelGGL(fmt_cond_kernel<float>, dim3(g), dim3(256), 0, st, clin, temb, rows, H, (float *) y);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_xpos(const float *x1, const float *pos, int T, int H, int B, float *x, hipStream_t st) {
+    hipLaunchKernelGGL(fmt_xpos_kernel, dim3(fmt_grid((int64_t) T * H * B)), dim3(256), 0, st, x1, pos, T, H, B, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_ln_mod(const float *x, const float *mod, int64_t mstride, int shift_off, int scale_off,
+                             int rows, int H, float eps, void *y, bool f16, hipStream_t st) {
+    if (H > 16 * 256) return hipErrorInvalidValue;
+    if (f16)
+        hipLaunchKernelGGL(fmt_ln_mod_kernel<half_t>, dim3((unsigned) rows), dim3(256), 0, st, x, mod, mstride,
+                           shift_off, scale_off, H, eps, (half_t *) y);
+    else
+        hipLaunchKernelGGL(fmt_ln_mod_kernel<float>, dim3((unsigned) rows), dim3(256), 0, st, x, mod, mstride,
+                           shift_off, scale_off, H, eps, (float *) y);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_attn(const float *qkv, int B, int T, int H, int nh, int w, void *o, bool f16, hipStream_t st) {
+    if (H % nh != 0 || H / nh > 256 || 2 * w + 1 > 15 || w < 0) return hipErrorInvalidValue;
+    const float scale = 1.0f / sqrtf((float) (H / nh));
+    const unsigned g = (unsigned) ((B * nh * T + 3) / 4);
+    if (f16) hipLaunchKernelGGL(fmt_attn_kernel<half_t>, dim3(g), dim3(256), 0, st, qkv, B, T, H, nh, w, scale, (half_t *) o);
+    else hipLaunchKernelGGL(fmt_attn_kernel<float>, dim3(g), dim3(256), 0, st, qkv, B, T, H, nh, w, scale, (float *) o);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_euler(const float *v, float *x60, int T, int P, int D, float a_cfg, float e_cfg, float dt,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(fmt_euler_kernel, dim3(fmt_grid((int64_t) (T - P) * D)), dim3(256), 0, st, v, x60, T, P, D,
+                       a_cfg, e_cfg, dt);
+    return hipGetLastError();
+}
+
+}  // namespace tpmd

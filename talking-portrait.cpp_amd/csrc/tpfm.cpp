@@ -1,0 +1,512 @@
+// Flow-matching transformer context behind the tpfm_* C ABI: the reference's
+// fmt_model (src/fmt.h:9-36) — weights, prepare, the CFG-batched forward
+// (src/fmt.cpp:44-205) — and its chunk sampler (src/pipeline.cpp:12-91), on
+// the k_fmt.hip kernels and the MFMA GEMM of k_enc.hip.  Host code only.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "tpmd.h"
+#include "tpmd_fmt.h"
+
+using namespace tpmd;
+
+namespace {
+
+std::string ffmt(const char *f, ...) __attribute__((format(printf, 1, 2)));
+std::string ffmt(const char *f, ...) {
+    char b[512];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(b, sizeof b, f, ap);
+    va_end(ap);
+    return b;
+}
+
+struct FTensor {
+    std::vector<float> data;
+    int flags = 0;
+};
+
+int round32(int v) { return (v + 31) / 32 * 32; }
+
+}  // namespace
+
+struct tpfm_ctx {
+    int device = 0;
+    bool f16 = false;
+    tpfm_config cfg{};
+    int T = 60, B = 3, CD = 1031, CDp = 1056, MLP = 4096;
+    std::string err;
+    hipStream_t stream = nullptr;
+    std::vector<std::pair<std::string, std::vector<int64_t>>> tensors;
+    std::map<std::string, FTensor> host;
+    bool prepared = false;
+    std::vector<void *> allocs;
+
+    struct Lin {  // a linear layer as the GEMM's A operand [out][in (padded)]
+        void *W = nullptr;
+        float *b = nullptr;
+        bool f16 = false;
+        int out = 0, in = 0;
+    };
+    Lin cemb, xemb, fin_mod, fin_lin;
+    struct Block {
+        Lin mod, qkv, proj, fc1, fc2;
+    };
+    std::vector<Block> blocks;
+    float *t0w = nullptr, *t0b = nullptr, *t2w = nullptr, *t2b = nullptr;  // t-embedder (GEMV, f32 values)
+    bool t0_16 = false, t2_16 = false;
+    float *pos = nullptr;
+    std::vector<float> t_freqs;
+
+    // activations
+    float *tf = nullptr, *te0 = nullptr, *te = nullptr;
+    float *cond_f = nullptr, *clin = nullptr, *x60 = nullptr, *x1 = nullptr, *x = nullptr;
+    float *mod = nullptr, *qkv = nullptr, *fmod = nullptr, *v = nullptr;
+    void *cond_a = nullptr, *sc_a = nullptr, *x60_a = nullptr, *h_a = nullptr, *o_a = nullptr, *m1_a = nullptr;
+
+    bool hip_ok(hipError_t e, const char *what) {
+        if (e == hipSuccess) return true;
+        err = ffmt("%s: %s", what, hipGetErrorString(e));
+        return false;
+    }
+    void *dalloc(size_t bytes) {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes < 256 ? 256 : bytes) != hipSuccess) {
+            err = ffmt("hipMalloc of %zu bytes failed", bytes);
+            return nullptr;
+        }
+        allocs.push_back(p);
+        return p;
+    }
+    template <typename T>
+    T *upload(const std::vector<T> &v) {
+        T *p = (T *) dalloc(v.size() * sizeof(T));
+        if (!p) return nullptr;
+        if (!hip_ok(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "upload")) return nullptr;
+        return p;
+    }
+    const FTensor *need(const std::string &name) {
+        auto it = host.find(name);
+        if (it == host.end()) {
+            if (err.empty()) err = "missing tensor " + name;
+            return nullptr;
+        }
+        return &it->second;
+    }
+    bool kept16(const FTensor &t) const { return f16 && (t.flags & TPMD_W_F16_FILE) && t.data.size() >= 4096; }
+    std::vector<float> dev_value(const FTensor &t) const {
+        std::vector<float> v = t.data;
+        if (kept16(t))
+            for (auto &x : v) x = (float) (_Float16) x;
+        return v;
+    }
+    size_t asz(bool h) const { return h ? 2 : 4; }
+    void free_all() {
+        for (void *p : allocs) (void) hipFree(p);
+        allocs.clear();
+    }
+    ~tpfm_ctx() {
+        if (device >= 0) (void) hipSetDevice(device);
+        free_all();
+        if (stream) (void) hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+bool check(tpfm_ctx *c) {
+    if (!c) return false;
+    c->err.clear();
+    if (hipSetDevice(c->device) != hipSuccess) {
+        c->err = "hipSetDevice failed";
+        return false;
+    }
+    return true;
+}
+
+void make_tensor_list(tpfm_ctx *c) {
+    const int64_t H = c->cfg.dim_h, M = c->MLP;
+    auto &v = c->tensors;
+    auto add = [&](const std::string &n, std::vector<int64_t> s) { v.push_back({n, std::move(s)}); };
+    add("t_embedder.mlp.0.weight", {H, c->cfg.t_freq_dim});
+    add("t_embedder.mlp.0.bias", {H});
+    add("t_embedder.mlp.2.weight", {H, H});
+    add("t_embedder.mlp.2.bias", {H});
+    add("c_embedder.weight", {H, c->CD});
+    add("c_embedder.bias", {H});
+    add("x_embedder.proj.weight", {H, c->cfg.dim_w});
+    add("x_embedder.proj.bias", {H});
+    add("pos_embed", {1, c->T, H});
+    for (int i = 0; i < c->cfg.depth; i++) {
+        const std::string b = ffmt("blocks.%d", i);
+        add(b + ".adaLN_modulation.1.weight", {6 * H, H});
+        add(b + ".adaLN_modulation.1.bias", {6 * H});
+        add(b + ".attn.qkv.weight", {3 * H, H});
+        add(b + ".attn.qkv.bias", {3 * H});
+        add(b + ".attn.proj.weight", {H, H});
+        add(b + ".attn.proj.bias", {H});
+        add(b + ".mlp.fc1.weight", {M, H});
+        add(b + ".mlp.fc1.bias", {M});
+        add(b + ".mlp.fc2.weight", {H, M});
+        add(b + ".mlp.fc2.bias", {H});
+    }
+    add("decoder.adaLN_modulation.1.weight", {2 * H, H});
+    add("decoder.adaLN_modulation.1.bias", {2 * H});
+    add("decoder.linear.weight", {c->cfg.dim_w, H});
+    add("decoder.linear.bias", {c->cfg.dim_w});
+}
+
+// weight [out][in] -> operand [out][in_pad] (zero columns past in), f16 when kept f16
+bool make_lin(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::string &base, int out, int in, int in_pad) {
+    const FTensor *w = c->need(base + ".weight"), *b = c->need(base + ".bias");
+    if (!w || !b) return false;
+    L.out = out;
+    L.in = in_pad;
+    L.f16 = c->kept16(*w);
+    const std::vector<float> dv = c->dev_value(*w);
+    std::vector<float> a((size_t) out * in_pad, 0.0f);
+    for (int o = 0; o < out; o++)
+        for (int i = 0; i < in; i++) a[(size_t) o * in_pad + i] = dv[(size_t) o * in + i];
+    if (L.f16) {
+        std::vector<_Float16> h(a.size());
+        for (size_t i = 0; i < a.size(); i++) h[i] = (_Float16) a[i];
+        L.W = c->upload(h);
+    } else {
+        L.W = c->upload(a);
+    }
+    L.b = c->upload(b->data);
+    return L.W && L.b;
+}
+
+// y[rows][L.out] (+ gate, residual, activation, operand copy) = X[rows][L.in] L.W^T + L.b
+bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float *Y, void *Ya, bool ya16, int act,
+            const float *gate = nullptr, int64_t gstride = 0, const float *res = nullptr) {
+    EncConvParams p{};
+    p.A = L.W;
+    p.X = X;
+    p.Y = Y;
+    p.Ya = Ya;
+    p.ya_f16 = ya16 ? 1 : 0;
+    p.bias = L.b;
+    p.res = res;
+    p.leaky = act;
+    p.gate = gate;
+    p.gstride = gstride;
+    p.H = 1;
+    p.W = rows;
+    p.IC = L.in;
+    p.OC = L.out;
+    p.KH = p.KW = 1;
+    p.stride = 1;
+    p.pad = 0;
+    p.OH = 1;
+    p.OW = rows;
+    return c->hip_ok(launch_enc_conv(p, L.f16, c->stream), "linear");
+}
+
+// the CFG-batched forward on device buffers: x60 (f32 [T][dim_w]) and cond_a
+// (operand rows [B*T][CDp]) are in place; v (f32 [B*T][dim_w]) is the result
+bool enqueue_forward(tpfm_ctx *c, float t) {
+    const tpfm_config &g = c->cfg;
+    const int H = g.dim_h, T = c->T, R = c->B * T;
+    hipStream_t st = c->stream;
+    // t embedding: GLIDE features on the host (src/fmt.cpp:168-174), two GEMVs
+    const int half = g.t_freq_dim / 2;
+    std::vector<float> tf((size_t) g.t_freq_dim);
+    for (int k = 0; k < half; k++) {
+        const float a = t * c->t_freqs[(size_t) k];
+        tf[(size_t) k] = cosf(a);
+        tf[(size_t) (half + k)] = sinf(a);
+    }
+    if (!c->hip_ok(hipMemcpyAsync(c->tf, tf.data(), tf.size() * 4, hipMemcpyHostToDevice, st), "t_freq")) return false;
+    if (!c->hip_ok(launch_enc_linear(c->t0w, c->t0b, c->tf, H, g.t_freq_dim, c->t0_16, c->te0, st), "t_embed") ||
+        !c->hip_ok(launch_fmt_silu(c->te0, H, st), "silu") ||
+        !c->hip_ok(launch_enc_linear(c->t2w, c->t2b, c->te0, H, H, c->t2_16, c->te, st), "t_embed"))
+        return false;
+    // the tf staging vector must outlive the copy
+    if (!c->hip_ok(hipStreamSynchronize(st), "t_freq sync")) return false;
+    // c = c_embed(cond) + t_emb; the adaLN layers read silu(c)
+    const bool sc16 = c->blocks.empty() ? c->fin_mod.f16 : c->blocks[0].mod.f16;
+    if (!linear(c, c->cemb, c->cond_a, R, c->clin, nullptr, false, 0) ||
+        !c->hip_ok(launch_fmt_cond(c->clin, c->te, R, H, c->sc_a, sc16, st), "cond"))
+        return false;
+    // x = x_embed(x60) + pos, shared by the branches
+    if (!c->hip_ok(launch_fmt_convert(c->x60, T, g.dim_w, g.dim_w, c->x60_a, c->xemb.f16, st), "x60") ||
+        !linear(c, c->xemb, c->x60_a, T, c->x1, nullptr, false, 0) ||
+        !c->hip_ok(launch_fmt_xpos(c->x1, c->pos, T, H, c->B, c->x, st), "pos"))
+        return false;
+    const int64_t ms = 6 * (int64_t) H;
+    for (const auto &Bk : c->blocks) {
+        if (!linear(c, Bk.mod, c->sc_a, R, c->mod, nullptr, false, 0)) return false;
+        // attention branch
+        if (!c->hip_ok(launch_fmt_ln_mod(c->x, c->mod, ms, 0, H, R, H, g.ln_eps, c->h_a, Bk.qkv.f16, st), "norm") ||
+            !linear(c, Bk.qkv, c->h_a, R, c->qkv, nullptr, false, 0) ||
+            !c->hip_ok(launch_fmt_attn(c->qkv, c->B, T, H, g.n_heads, g.attn_window, c->o_a, Bk.proj.f16, st),
+                       "attention") ||
+            !linear(c, Bk.proj, c->o_a, R, c->x, nullptr, false, 0, c->mod + 2 * H, ms, c->x))
+            return false;
+        // MLP branch
+        if (!c->hip_ok(launch_fmt_ln_mod(c->x, c->mod, ms, 3 * H, 4 * H, R, H, g.ln_eps, c->h_a, Bk.fc1.f16, st),
+                       "norm") ||
+            !linear(c, Bk.fc1, c->h_a, R, nullptr, c->m1_a, Bk.fc2.f16, 2) ||
+            !linear(c, Bk.fc2, c->m1_a, R, c->x, nullptr, false, 0, c->mod + 5 * H, ms, c->x))
+            return false;
+    }
+    // final head
+    if (!linear(c, c->fin_mod, c->sc_a, R, c->fmod, nullptr, false, 0) ||
+        !c->hip_ok(launch_fmt_ln_mod(c->x, c->fmod, 2 * (int64_t) H, 0, H, R, H, g.ln_eps, c->h_a, c->fin_lin.f16, st),
+                   "norm") ||
+        !linear(c, c->fin_lin, c->h_a, R, c->v, nullptr, false, 0))
+        return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+void tpfm_default_config(tpfm_config *g) {
+    if (!g) return;
+    g->dim_h = 1024;
+    g->depth = 8;
+    g->n_heads = 8;
+    g->dim_w = 512;
+    g->dim_a = 512;
+    g->dim_e = 7;
+    g->chunk_frames = 50;
+    g->prev_frames = 10;
+    g->attn_window = 2;
+    g->t_freq_dim = 256;
+    g->nfe = 10;
+    g->mlp_ratio = 4.0f;
+    g->ln_eps = 1e-6f;
+    g->a_cfg = 2.0f;
+    g->e_cfg = 1.0f;
+    g->r_cfg = 1.0f;
+}
+
+tpfm_ctx *tpfm_create(int device, const char *ftype, const tpfm_config *cfg) {
+    if (!ftype || (strcmp(ftype, "f32") != 0 && strcmp(ftype, "f16") != 0) || !cfg) {
+        fprintf(stderr, "tpfm_create: ftype must be f32 or f16, and a config is needed\n");
+        return nullptr;
+    }
+    const tpfm_config &g = *cfg;
+    const int mlp = (int) ((float) g.dim_h * g.mlp_ratio);
+    if (g.dim_h <= 0 || g.n_heads <= 0 || g.dim_h % g.n_heads != 0 || g.dim_h / g.n_heads > 256 ||
+        g.dim_h % 32 != 0 || g.dim_w % 32 != 0 || g.t_freq_dim % 32 != 0 || mlp % 32 != 0 || g.attn_window < 0 ||
+        g.attn_window > 7 || g.depth < 0 || g.dim_a <= 0 || g.dim_e < 0 || g.chunk_frames <= 0 ||
+        g.prev_frames < 0 || g.nfe < 2 || g.dim_h > 4096) {
+        fprintf(stderr, "tpfm_create: unsupported FMT configuration\n");
+        return nullptr;
+    }
+    tpfm_ctx *c = new tpfm_ctx();
+    c->device = device;
+    c->f16 = strcmp(ftype, "f16") == 0;
+    c->cfg = g;
+    c->T = g.chunk_frames + g.prev_frames;
+    c->CD = g.dim_w + g.dim_a + g.dim_e;
+    c->CDp = round32(c->CD);
+    c->MLP = mlp;
+    if (hipSetDevice(device) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        fprintf(stderr, "tpfm_create: no HIP device %d\n", device);
+        c->device = -1;
+        delete c;
+        return nullptr;
+    }
+    const int half = g.t_freq_dim / 2;
+    c->t_freqs.resize((size_t) half);
+    for (int k = 0; k < half; k++)
+        c->t_freqs[(size_t) k] = (float) exp(-log(10000.0) * (double) k / (double) half);
+    make_tensor_list(c);
+    return c;
+}
+
+void tpfm_destroy(tpfm_ctx *c) { delete c; }
+
+const char *tpfm_last_error(const tpfm_ctx *c) { return c ? c->err.c_str() : "no context"; }
+
+const char *tpfm_weight_name(const tpfm_ctx *c, int i, int64_t *n, int *is_matrix) {
+    if (!c || i < 0 || i >= (int) c->tensors.size()) return nullptr;
+    const auto &t = c->tensors[(size_t) i];
+    int64_t e = 1;
+    for (auto d : t.second) e *= d;
+    if (n) *n = e;
+    if (is_matrix) *is_matrix = t.second.size() >= 2 ? 1 : 0;
+    return t.first.c_str();
+}
+
+int tpfm_set_weight(tpfm_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+    if (!check(c)) return -1;
+    if (!name || !data || n <= 0) {
+        c->err = "tpfm_set_weight: null name/data or empty tensor";
+        return -1;
+    }
+    const std::vector<int64_t> *shape = nullptr;
+    for (const auto &t : c->tensors)
+        if (t.first == name) shape = &t.second;
+    if (!shape) {
+        c->err = ffmt("tpfm_set_weight: unknown FMT tensor %s", name);
+        return -1;
+    }
+    int64_t want = 1;
+    for (auto d : *shape) want *= d;
+    if (want != n) {
+        c->err = ffmt("tpfm_set_weight: %s has %lld elements, expected %lld", name, (long long) n, (long long) want);
+        return -1;
+    }
+    FTensor t;
+    t.data.assign(data, data + n);
+    t.flags = flags;
+    c->host[name] = std::move(t);
+    c->prepared = false;
+    return 0;
+}
+
+int tpfm_prepare(tpfm_ctx *c) {
+    if (!check(c)) return -1;
+    c->free_all();
+    c->prepared = false;
+    const tpfm_config &g = c->cfg;
+    const int H = g.dim_h, T = c->T, R = c->B * T;
+    c->blocks.assign((size_t) g.depth, tpfm_ctx::Block{});
+    {
+        const FTensor *w0 = c->need("t_embedder.mlp.0.weight"), *b0 = c->need("t_embedder.mlp.0.bias"),
+                      *w2 = c->need("t_embedder.mlp.2.weight"), *b2 = c->need("t_embedder.mlp.2.bias"),
+                      *pe = c->need("pos_embed");
+        if (!w0 || !b0 || !w2 || !b2 || !pe) return -1;
+        c->t0_16 = c->kept16(*w0);
+        c->t2_16 = c->kept16(*w2);
+        c->t0w = c->upload(c->dev_value(*w0));
+        c->t0b = c->upload(b0->data);
+        c->t2w = c->upload(c->dev_value(*w2));
+        c->t2b = c->upload(b2->data);
+        c->pos = c->upload(c->dev_value(*pe));
+        if (!c->t0w || !c->t0b || !c->t2w || !c->t2b || !c->pos) return -1;
+    }
+    if (!make_lin(c, c->cemb, "c_embedder", H, c->CD, c->CDp) ||
+        !make_lin(c, c->xemb, "x_embedder.proj", H, g.dim_w, g.dim_w))
+        return -1;
+    for (int i = 0; i < g.depth; i++) {
+        auto &B = c->blocks[(size_t) i];
+        const std::string b = ffmt("blocks.%d", i);
+        if (!make_lin(c, B.mod, b + ".adaLN_modulation.1", 6 * H, H, H) ||
+            !make_lin(c, B.qkv, b + ".attn.qkv", 3 * H, H, H) || !make_lin(c, B.proj, b + ".attn.proj", H, H, H) ||
+            !make_lin(c, B.fc1, b + ".mlp.fc1", c->MLP, H, H) || !make_lin(c, B.fc2, b + ".mlp.fc2", H, c->MLP, c->MLP))
+            return -1;
+    }
+    if (!make_lin(c, c->fin_mod, "decoder.adaLN_modulation.1", 2 * H, H, H) ||
+        !make_lin(c, c->fin_lin, "decoder.linear", g.dim_w, H, H))
+        return -1;
+    // silu(c) is one operand buffer for every adaLN layer: they share a type
+    for (const auto &B : c->blocks)
+        if (B.mod.f16 != c->fin_mod.f16) {
+            c->err = "tpfm_prepare: adaLN weights stored with mixed types";
+            return -1;
+        }
+    auto F = [&](size_t n) { return (float *) c->dalloc(n * 4); };
+    auto A = [&](size_t n) { return c->dalloc(n * 4); };  // operand buffers sized for f32
+    c->tf = F((size_t) g.t_freq_dim);
+    c->te0 = F((size_t) H);
+    c->te = F((size_t) H);
+    c->cond_f = F((size_t) R * c->CD);
+    c->cond_a = A((size_t) R * c->CDp);
+    c->clin = F((size_t) R * H);
+    c->sc_a = A((size_t) R * H);
+    c->x60 = F((size_t) T * g.dim_w);
+    c->x60_a = A((size_t) T * g.dim_w);
+    c->x1 = F((size_t) T * H);
+    c->x = F((size_t) R * H);
+    c->mod = F((size_t) R * 6 * H);
+    c->h_a = A((size_t) R * std::max(H, g.dim_w));
+    c->qkv = F((size_t) R * 3 * H);
+    c->o_a = A((size_t) R * H);
+    c->m1_a = A((size_t) R * c->MLP);
+    c->fmod = F((size_t) R * 2 * H);
+    c->v = F((size_t) R * g.dim_w);
+    if (!c->tf || !c->te0 || !c->te || !c->cond_f || !c->cond_a || !c->clin || !c->sc_a || !c->x60 || !c->x60_a ||
+        !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->fmod || !c->v)
+        return -1;
+    c->prepared = true;
+    return 0;
+}
+
+int tpfm_forward(tpfm_ctx *c, const float *x60, const float *cond, float t, float *v_out) {
+    if (!check(c)) return -1;
+    if (!c->prepared) {
+        c->err = "FMT not prepared";
+        return -1;
+    }
+    if (!x60 || !cond || !v_out) {
+        c->err = "tpfm_forward: null buffer";
+        return -1;
+    }
+    const int T = c->T, R = c->B * T, D = c->cfg.dim_w;
+    hipStream_t st = c->stream;
+    if (!c->hip_ok(hipMemcpyAsync(c->x60, x60, (size_t) T * D * 4, hipMemcpyHostToDevice, st), "x60") ||
+        !c->hip_ok(hipMemcpyAsync(c->cond_f, cond, (size_t) R * c->CD * 4, hipMemcpyHostToDevice, st), "cond") ||
+        !c->hip_ok(launch_fmt_convert(c->cond_f, R, c->CD, c->CDp, c->cond_a, c->cemb.f16, st), "cond"))
+        return -1;
+    if (!enqueue_forward(c, t)) return -1;
+    if (!c->hip_ok(hipMemcpyAsync(v_out, c->v, (size_t) R * D * 4, hipMemcpyDeviceToHost, st), "v") ||
+        !c->hip_ok(hipStreamSynchronize(st), "forward sync"))
+        return -1;
+    return 0;
+}
+
+int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const float *prev_wa,
+                      const float *cond_audio, int emotion, const float *x0, float *motion_out) {
+    if (!check(c)) return -1;
+    if (!c->prepared) {
+        c->err = "FMT not prepared";
+        return -1;
+    }
+    const tpfm_config &g = c->cfg;
+    const int T = c->T, P = g.prev_frames, CF = g.chunk_frames, D = g.dim_w, DA = g.dim_a, CD = c->CD;
+    if (!wr || (P > 0 && (!prev_x || !prev_wa)) || !cond_audio || !x0 || !motion_out) {
+        c->err = "tpfm_sample_chunk: null buffer";
+        return -1;
+    }
+    // condition rows [wr | wa | we] per branch and frame (src/pipeline.cpp:22-36)
+    std::vector<float> cond((size_t) 3 * T * CD, 0.0f), x60((size_t) T * D);
+    for (int b = 0; b < 3; b++)
+        for (int f = 0; f < T; f++) {
+            float *row = cond.data() + ((size_t) b * T + f) * CD;
+            memcpy(row, wr, (size_t) D * 4);
+            const float *wa = f < P ? prev_wa + (size_t) f * DA : cond_audio + (size_t) (f - P) * DA;
+            if (!(b == 0 && f >= P)) memcpy(row + D, wa, (size_t) DA * 4);
+            if (b == 1 && emotion >= 0 && emotion < g.dim_e) row[D + DA + emotion] = 1.0f;
+        }
+    if (P > 0) memcpy(x60.data(), prev_x, (size_t) P * D * 4);
+    memcpy(x60.data() + (size_t) P * D, x0, (size_t) CF * D * 4);
+    hipStream_t st = c->stream;
+    const int R = 3 * T;
+    if (!c->hip_ok(hipMemcpyAsync(c->x60, x60.data(), x60.size() * 4, hipMemcpyHostToDevice, st), "x60") ||
+        !c->hip_ok(hipMemcpyAsync(c->cond_f, cond.data(), cond.size() * 4, hipMemcpyHostToDevice, st), "cond") ||
+        !c->hip_ok(launch_fmt_convert(c->cond_f, R, CD, c->CDp, c->cond_a, c->cemb.f16, st), "cond"))
+        return -1;
+    // torch linspace(0, 1, nfe) in f32 (src/pipeline.cpp:12-13)
+    auto ode_t = [&](int i) { return (float) ((double) i / (double) (g.nfe - 1)); };
+    for (int s = 0; s < g.nfe - 1; s++) {
+        if (!enqueue_forward(c, ode_t(s))) return -1;
+        const float dt = ode_t(s + 1) - ode_t(s);
+        if (!c->hip_ok(launch_fmt_euler(c->v, c->x60, T, P, D, g.a_cfg, g.e_cfg, dt, st), "euler")) return -1;
+    }
+    if (!c->hip_ok(hipMemcpyAsync(motion_out, c->x60 + (size_t) P * D, (size_t) CF * D * 4, hipMemcpyDeviceToHost,
+                                  st),
+                   "motion") ||
+        !c->hip_ok(hipStreamSynchronize(st), "sample sync"))
+        return -1;
+    return 0;
+}
+
+}  // extern "C"

@@ -6,18 +6,20 @@
 
 namespace tpmd {
 
-// y[n][o] = act(sum_k A[o][k] X(k, n) + bias[o]) + res[n][o] over channel-last
+// y[n][o] = gate[n][o] * act(sum_k A[o][k] X(k, n) + bias[o]) + res[n][o] over channel-last
 // maps: A [OC][KH][KW][IC] (tap-major k = (kh*KW + kw)*IC + ic), X [H][W][IC],
 // y [OH][OW][OC] f32, OH = (H + 2 pad - KH) / stride + 1
 struct EncConvParams {
     const void *A;          // operand type (f16 or f32)
     const void *X;          // operand type
-    float *Y;               // f32 output
+    float *Y;               // f32 output, or null (Ya only)
     void *Ya;               // optional copy of Y in the next conv's operand type
     int ya_f16;             // Ya is f16 (else f32)
     const float *bias;      // [OC] or null
     const float *res;       // [OH][OW][OC] f32 added after the activation, or null
-    int leaky;              // leaky_relu 0.2 after the bias
+    int leaky;              // activation after the bias: 0 none, 1 leaky_relu 0.2, 2 tanh-GELU
+    const float *gate;      // gate[n * gstride + o] multiplies the activation, or null
+    int64_t gstride;
     int H, W, IC, OC, KH, KW, stride, pad, OH, OW;
 };
 

@@ -1,5 +1,6 @@
 // GGUF v3 reader (see gguf.h) and the C entry points tpmd_load_gguf /
-// tpme_load_gguf / tpmd_gguf_read_tensor of include/tpmd.h.
+// tpme_load_gguf / tpfm_read_config / tpfm_load_gguf / tpmd_gguf_read_tensor
+// of include/tpmd.h.
 #include "gguf.h"
 
 #include <cstdio>
@@ -259,6 +260,69 @@ int tpme_load_gguf(tpme_ctx *ctx, const char *path, char *err, size_t err_size) 
                         " elements, expected " + std::to_string(n));
         if (tpme_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
             return fail(tpme_last_error(ctx));
+    }
+    return 0;
+}
+
+int tpfm_read_config(const char *path, tpfm_config *cfg, char *err, size_t err_size) {
+    auto fail = [&](const std::string &m) {
+        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
+        return -1;
+    };
+    if (!path || !cfg) return fail("tpfm_read_config: null path or config");
+    tp::gguf_file f;
+    std::string e;
+    if (!f.open(path, "float-fmt", e)) return fail(e);
+    tpfm_default_config(cfg);
+    auto num = [&](const char *key, double def) {
+        auto it = f.kv_num.find(std::string("float.fmt.") + key);
+        return it == f.kv_num.end() ? def : it->second;
+    };
+    // src/fmt.cpp:10-26
+    cfg->dim_h = (int) num("dim_h", cfg->dim_h);
+    cfg->depth = (int) num("depth", cfg->depth);
+    cfg->n_heads = (int) num("n_heads", cfg->n_heads);
+    cfg->dim_w = (int) num("dim_w", cfg->dim_w);
+    cfg->dim_a = (int) num("dim_a", cfg->dim_a);
+    cfg->dim_e = (int) num("dim_e", cfg->dim_e);
+    cfg->chunk_frames = (int) num("chunk_frames", cfg->chunk_frames);
+    cfg->prev_frames = (int) num("prev_frames", cfg->prev_frames);
+    cfg->attn_window = (int) num("attn_window", cfg->attn_window);
+    cfg->t_freq_dim = (int) num("t_freq_dim", cfg->t_freq_dim);
+    cfg->nfe = (int) num("nfe", cfg->nfe);
+    cfg->a_cfg = (float) num("a_cfg_scale", cfg->a_cfg);
+    cfg->e_cfg = (float) num("e_cfg_scale", cfg->e_cfg);
+    cfg->r_cfg = (float) num("r_cfg_scale", cfg->r_cfg);
+    cfg->ln_eps = (float) num("ln_eps", cfg->ln_eps);
+    cfg->mlp_ratio = (float) num("mlp_ratio", cfg->mlp_ratio);
+    const double total = num("num_total_frames", cfg->chunk_frames + cfg->prev_frames);
+    if ((int) total != cfg->chunk_frames + cfg->prev_frames)
+        return fail(std::string(path) + ": num_total_frames != chunk_frames + prev_frames");
+    return 0;
+}
+
+int tpfm_load_gguf(tpfm_ctx *ctx, const char *path, char *err, size_t err_size) {
+    auto fail = [&](const std::string &m) {
+        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
+        return -1;
+    };
+    if (!ctx || !path) return fail("tpfm_load_gguf: null context or path");
+    tp::gguf_file f;
+    std::string e;
+    if (!f.open(path, "float-fmt", e)) return fail(e);
+    std::vector<float> v;
+    for (int i = 0;; i++) {
+        int64_t n = 0;
+        const char *name = tpfm_weight_name(ctx, i, &n, nullptr);
+        if (!name) break;
+        if (!f.find(name)) continue;  // prepare() names the first missing tensor
+        bool f16 = false;
+        if (!f.read(name, v, f16, e)) return fail(e);
+        if ((int64_t) v.size() != n)
+            return fail(std::string(path) + ": tensor " + name + " has " + std::to_string(v.size()) +
+                        " elements, expected " + std::to_string(n));
+        if (tpfm_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
+            return fail(tpfm_last_error(ctx));
     }
     return 0;
 }

@@ -222,6 +222,46 @@ def image(seed=1005, res=512):
     return np.ascontiguousarray(np.clip(f, -1.0, 1.0).transpose(2, 0, 1).astype(np.float32))
 
 
+# ---- flow-matching transformer (src/fmt.cpp, src/pipeline.cpp:12-91)
+
+def fmt_raw_weights(cfg, seed=1006, ftype="f32"):
+    """name -> (float32 array in torch shape, f16_in_file) for an FMT of
+    config `cfg` (oracle.fmt.Config), seed 1006: Linear weights
+    ~ N(0,1)/sqrt(fan_in) (adaLN weights x0.5, so the gates and shifts are
+    O(0.1-1) instead of the adaLN-Zero start), biases ~ N(0,1) * 0.02,
+    pos_embed ~ N(0,1) * 0.1."""
+    from oracle import fmt as OF
+    out = {}
+    for name, shape in OF.weight_names(cfg):
+        g = _rng(seed, name)
+        a = g.standard_normal(shape, dtype=np.float32)
+        if name.endswith(".weight"):
+            a = a / np.float32(np.sqrt(shape[1]))
+            if "adaLN" in name:
+                a = a * np.float32(0.5)
+        elif name == "pos_embed":
+            a = a * np.float32(0.1)
+        else:
+            a = a * np.float32(0.02)
+        a = a.astype(np.float32)
+        f16 = ftype == "f16" and len(shape) >= 2 and name != "pos_embed"
+        if f16:
+            a = a.astype(np.float16).astype(np.float32)
+        out[name] = (np.ascontiguousarray(a), f16)
+    return out
+
+
+def fmt_chunk_inputs(cfg, seed=1007):
+    """one chunk's sampler inputs (src/pipeline.cpp:15-20): wr (dim_w,),
+    prev_x (prev, dim_w), prev_wa (prev, dim_a), cond_audio (chunk, dim_a),
+    x0 (chunk, dim_w) noise"""
+    g = _rng(seed, "fmt_chunk")
+    f = lambda *sh: np.ascontiguousarray(g.standard_normal(sh).astype(np.float32))
+    P, CF = cfg.prev_frames, cfg.chunk_frames
+    return dict(wr=f(cfg.dim_w), prev_x=f(P, cfg.dim_w), prev_wa=f(P, cfg.dim_a),
+                cond_audio=f(CF, cfg.dim_a), x0=f(CF, cfg.dim_w))
+
+
 def grid(n, lo, hi, seed=1003, jitter=0.0, res=None):
     """(n, 2) interleaved grid-sample coordinates ~ U(lo, hi) [+ U(-.5,.5)*jitter/res]."""
     g = _rng(seed, "grid")

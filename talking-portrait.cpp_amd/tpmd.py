@@ -89,6 +89,17 @@ def lib():
             "tpme_feat": (P, [P, I, P, P]),
             "tpme_level": (I64, [P, I, P]),
             "tpme_load_gguf": (I, [P, C, P, ctypes.c_size_t]),
+            "tpfm_default_config": (None, [P]),
+            "tpfm_read_config": (I, [C, P, P, ctypes.c_size_t]),
+            "tpfm_create": (P, [I, C, P]),
+            "tpfm_destroy": (None, [P]),
+            "tpfm_last_error": (C, [P]),
+            "tpfm_weight_name": (C, [P, I, P, P]),
+            "tpfm_set_weight": (I, [P, C, P, I64, I]),
+            "tpfm_load_gguf": (I, [P, C, P, ctypes.c_size_t]),
+            "tpfm_prepare": (I, [P]),
+            "tpfm_forward": (I, [P, P, P, ctypes.c_float, P]),
+            "tpfm_sample_chunk": (I, [P, P, P, P, P, I, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -468,3 +479,98 @@ class MotionEncoder:
                 raise TpmdError("encoder has not run")
             ptrs.append(p)
         return ptrs
+
+
+class FmtConfig(ctypes.Structure):
+    """tpfm_config (include/tpmd.h), fmt_model's hyper-parameters"""
+    _fields_ = [(n, ctypes.c_int) for n in ("dim_h", "depth", "n_heads", "dim_w", "dim_a", "dim_e",
+                                            "chunk_frames", "prev_frames", "attn_window", "t_freq_dim", "nfe")] + \
+               [(n, ctypes.c_float) for n in ("mlp_ratio", "ln_eps", "a_cfg", "e_cfg", "r_cfg")]
+
+    @classmethod
+    def default(cls, **kw):
+        c = cls()
+        lib().tpfm_default_config(ctypes.byref(c))
+        for k, v in kw.items():
+            setattr(c, k, v)
+        return c
+
+    @classmethod
+    def from_gguf(cls, path):
+        c = cls()
+        err = ctypes.create_string_buffer(512)
+        if lib().tpfm_read_config(str(path).encode(), ctypes.byref(c), err, len(err)) < 0:
+            raise TpmdError(err.value.decode())
+        return c
+
+    @property
+    def total(self):
+        return self.chunk_frames + self.prev_frames
+
+
+class FlowTransformer:
+    """tp::fmt_model (src/fmt.h:9-36) over tpfm_*: forward and sample_chunk"""
+
+    def __init__(self, ftype="f32", cfg=None, device=0):
+        self.cfg = cfg if cfg is not None else FmtConfig.default()
+        h = lib().tpfm_create(device, ftype.encode(), ctypes.byref(self.cfg))
+        if not h:
+            raise TpmdError("tpfm_create failed")
+        self.h = h
+        self.ftype = ftype
+
+    def _check(self, rc):
+        if rc < 0:
+            raise TpmdError(lib().tpfm_last_error(self.h).decode())
+        return rc
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().tpfm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weight_names(self):
+        out, i = [], 0
+        n = ctypes.c_int64()
+        while True:
+            nm = lib().tpfm_weight_name(self.h, i, ctypes.byref(n), None)
+            if nm is None:
+                return out
+            out.append((nm.decode(), n.value))
+            i += 1
+
+    def set_weights(self, raw):
+        for name, _ in self.weight_names():
+            arr, f16 = raw[name]
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            self._check(lib().tpfm_set_weight(self.h, name.encode(), _hptr(a), a.size, W_F16_FILE if f16 else 0))
+
+    def load_gguf(self, path):
+        err = ctypes.create_string_buffer(512)
+        if lib().tpfm_load_gguf(self.h, str(path).encode(), err, len(err)) < 0:
+            raise TpmdError(err.value.decode())
+
+    def prepare(self):
+        self._check(lib().tpfm_prepare(self.h))
+
+    def forward(self, x60, cond, t):
+        c = self.cfg
+        x = np.ascontiguousarray(x60, dtype=np.float32).reshape(c.total, c.dim_w)
+        cd = np.ascontiguousarray(cond, dtype=np.float32).reshape(3, c.total, c.dim_w + c.dim_a + c.dim_e)
+        v = np.empty((3, c.total, c.dim_w), np.float32)
+        self._check(lib().tpfm_forward(self.h, _hptr(x), _hptr(cd), float(t), _hptr(v)))
+        return v
+
+    def sample_chunk(self, wr, prev_x, prev_wa, cond_audio, emotion, x0):
+        c = self.cfg
+        a = [np.ascontiguousarray(v, dtype=np.float32) for v in (wr, prev_x, prev_wa, cond_audio, x0)]
+        out = np.empty((c.chunk_frames, c.dim_w), np.float32)
+        self._check(lib().tpfm_sample_chunk(self.h, _hptr(a[0]), _hptr(a[1]), _hptr(a[2]), _hptr(a[3]), int(emotion),
+                                            _hptr(a[4]), _hptr(out)))
+        return out

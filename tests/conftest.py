@@ -22,6 +22,13 @@ def om():
 
 
 @pytest.fixture(scope="session")
+def oracle_fmt():
+    from oracle import fmt, mdec
+    mdec.lib()
+    return fmt
+
+
+@pytest.fixture(scope="session")
 def oracle_menc():
     from oracle import mdec, menc
     mdec.lib()

@@ -1,0 +1,95 @@
+"""Flow-matching transformer (tpfm_*) on the GPU against the CPU oracle
+(oracle/fmt.py, the reference's graph src/fmt.cpp:44-205 and sampler
+src/pipeline.cpp:12-91): forward f32 rel-L2 <= 1e-4, f16 rel-L2 <= 1e-2 with
+cosine >= 0.9999; the sampled chunk likewise; GGUF loading bit-exact."""
+import numpy as np
+import pytest
+
+import gguf_writer
+import synth
+import tpmd
+from metrics import cosine, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(ftype, got, want, what):
+    e = rel_l2(got, want)
+    if ftype == "f32":
+        assert e <= 1e-4, (what, e)
+    else:
+        assert e <= 1e-2 and cosine(got, want) >= 0.9999, (what, e, cosine(got, want))
+
+
+def _small(OF):
+    return dict(dim_h=256, depth=2, n_heads=4, dim_w=64, dim_a=64, chunk_frames=12, prev_frames=4, t_freq_dim=64,
+                nfe=4)
+
+
+def _pair(oracle_fmt, ftype, kw):
+    ocfg = oracle_fmt.Config(**kw)
+    raw = synth.fmt_raw_weights(ocfg, ftype=ftype)
+    ref = oracle_fmt.FMT(raw, ocfg, ftype)
+    fm = tpmd.FlowTransformer(ftype, tpmd.FmtConfig.default(**kw))
+    fm.set_weights(raw)
+    fm.prepare()
+    return ocfg, raw, ref, fm
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_fmt_forward_small(oracle_fmt, torch_cuda, ftype):
+    ocfg, _, ref, fm = _pair(oracle_fmt, ftype, _small(oracle_fmt))
+    g = np.random.default_rng(4)
+    x60 = g.standard_normal((ocfg.total, ocfg.dim_w)).astype(np.float32)
+    cond = g.standard_normal((3, ocfg.total, ocfg.dim_c)).astype(np.float32)
+    for t in (0.0, 0.5, 1.0):
+        _close(ftype, fm.forward(x60, cond, t), ref.forward(x60, cond, t), ("forward", t))
+
+
+@pytest.mark.parametrize("ftype", ["f16", "f32"])
+def test_fmt_forward_reference_dims(oracle_fmt, torch_cuda, ftype):
+    ocfg, _, ref, fm = _pair(oracle_fmt, ftype, {})
+    io = synth.fmt_chunk_inputs(ocfg)
+    cond = ref.cond_rows(io["wr"], io["prev_wa"], io["cond_audio"], 2)
+    x60 = np.concatenate([io["prev_x"], io["x0"]])
+    _close(ftype, fm.forward(x60, cond, 0.3), ref.forward(x60, cond, 0.3), "forward")
+
+
+@pytest.mark.parametrize("ftype", ["f32", "f16"])
+def test_fmt_sample_chunk(oracle_fmt, torch_cuda, ftype):
+    ocfg, _, ref, fm = _pair(oracle_fmt, ftype, _small(oracle_fmt))
+    io = synth.fmt_chunk_inputs(ocfg)
+    for emo in (-1, 3):
+        args = (io["wr"], io["prev_x"], io["prev_wa"], io["cond_audio"], emo, io["x0"])
+        _close(ftype, fm.sample_chunk(*args), ref.sample_chunk(*args), ("chunk", emo))
+
+
+def test_fmt_gguf(oracle_fmt, torch_cuda, tmp_path):
+    """tpfm_read_config + tpfm_load_gguf on a float-fmt file == named weights"""
+    kw = _small(oracle_fmt)
+    ocfg = oracle_fmt.Config(**kw)
+    raw = synth.fmt_raw_weights(ocfg, ftype="f16")
+    path = tmp_path / "fmt_f16.gguf"
+    kv = [(f"float.fmt.{k}", 4, v) for k, v in kw.items()] + [("float.fmt.num_total_frames", 4, ocfg.total)]
+    gguf_writer.write(path, raw, arch="float-fmt", f16=True, extra_kv=kv)
+    cfg = tpmd.FmtConfig.from_gguf(path)
+    for k, v in kw.items():
+        assert getattr(cfg, k) == v, k
+    io = synth.fmt_chunk_inputs(ocfg)
+    args = (io["wr"], io["prev_x"], io["prev_wa"], io["cond_audio"], 1, io["x0"])
+    outs = []
+    for use_file in (False, True):
+        fm = tpmd.FlowTransformer("f16", cfg)
+        fm.load_gguf(path) if use_file else fm.set_weights(raw)
+        fm.prepare()
+        outs.append(fm.sample_chunk(*args))
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_fmt_error_contract(torch_cuda):
+    fm = tpmd.FlowTransformer("f32", tpmd.FmtConfig.default(dim_h=64, depth=1, n_heads=2, t_freq_dim=32))
+    with pytest.raises(tpmd.TpmdError, match="not prepared"):
+        fm.forward(np.zeros((60, 512), np.float32), np.zeros((3, 60, 1031), np.float32), 0.0)
+    with pytest.raises(tpmd.TpmdError, match="missing tensor t_embedder.mlp.0.weight"):
+        fm.prepare()
+    assert not tpmd.lib().tpfm_create(0, b"f16", tpmd.ctypes.byref(tpmd.FmtConfig.default(attn_window=9)))
