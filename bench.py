@@ -151,6 +151,43 @@ def encoder_timing(ftype, reps=20):
             "note": "tpme_run, 512x512 image resident in HBM, synchronous (host clock)"}
 
 
+def fmt_timing(ftype, reps=5):
+    """the flow-matching transformer at its default dims (src/fmt.h:10-16):
+    one CFG-batched forward and one 50-frame chunk (nfe - 1 = 9 forwards),
+    host in/out, median ms; GEMM FLOPs / forward time against the MFMA peak"""
+    import numpy as np
+    import synth
+    import tpmd
+    from oracle import fmt as OF   # names and shapes only (the tensor list)
+    cfg = OF.Config()
+    fm = tpmd.FlowTransformer(ftype)
+    fm.set_weights(synth.fmt_raw_weights(cfg, ftype=ftype))
+    fm.prepare()
+    io = synth.fmt_chunk_inputs(cfg)
+    g = np.random.default_rng(0)
+    x60 = g.standard_normal((cfg.total, cfg.dim_w)).astype(np.float32)
+    cond = g.standard_normal((3, cfg.total, cfg.dim_c)).astype(np.float32)
+    fm.forward(x60, cond, 0.5)
+    tf, tc = [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fm.forward(x60, cond, 0.5)
+        tf.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        fm.sample_chunk(io["wr"], io["prev_x"], io["prev_wa"], io["cond_audio"], 1, io["x0"])
+        tc.append(time.perf_counter() - t0)
+    H, T = cfg.dim_h, cfg.total
+    per_tok = cfg.depth * (6 * H * H + 3 * H * H + H * H + 2 * cfg.dim_mlp * H) + 2 * H * H + cfg.dim_w * H \
+        + cfg.dim_c * H
+    flops = 2.0 * 3 * T * per_tok + 2.0 * T * cfg.dim_w * H
+    ms = float(np.median(tf)) * 1e3
+    peak = 2500.0 if ftype == "f16" else 157.3
+    fm.close()
+    return {"forward_ms": round(ms, 3), "chunk_ms": round(float(np.median(tc)) * 1e3, 3),
+            "forward_gflop": round(flops / 1e9, 2), "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
+            "note": "tpfm_forward / tpfm_sample_chunk, host buffers, synchronous (host clock)"}
+
+
 def cpu_baseline(ftype_unused=None):
     """the CPU oracle's fast graph (f32, numpy/OpenBLAS + OpenMP C ops) on
     this host, one 512x512 frame"""
@@ -274,6 +311,7 @@ def main():
     out["host_delivered_fps"] = {"frames": n_seq, **host,
                                  "note": "pageable host buffer, PCIe download included"}
     out["encoder"] = encoder_timing(args.ftype)
+    out["fmt"] = fmt_timing(args.ftype)
     if args.copy_probe:
         copy_probe()
     if not args.no_cpu_baseline:
