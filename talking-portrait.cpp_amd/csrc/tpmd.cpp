@@ -98,11 +98,19 @@ struct tpmd_ctx {
     DemodTable dem{};
 
     int batch = 0;
-    float *lat = nullptr, *s_all = nullptr, *den_all = nullptr;
-    void *xs0 = nullptr, *c1 = nullptr, *trunk = nullptr;
-    float *outb = nullptr, *flow[2] = {}, *rgb[2] = {}, *img = nullptr;
-    float *ws = nullptr;              // split-K partials of the low-resolution convs
-    int64_t ws_elems = 0;
+    // per-batch buffers of one launch chain.  Device-resident decodes on the
+    // library's own stream alternate between two lanes, each with its own
+    // buffers and stream, so consecutive batches overlap on the GPU
+    struct Lane {
+        float *lat = nullptr, *s_all = nullptr, *den_all = nullptr;
+        void *xs0 = nullptr, *c1 = nullptr, *trunk = nullptr;
+        float *outb = nullptr, *flow[2] = {}, *rgb[2] = {}, *img = nullptr;
+        float *ws = nullptr;          // split-K partials of the low-resolution convs
+        int64_t ws_elems = 0;
+    } lane[2];
+    Lane *L = &lane[0];               // the lane the enqueued work uses
+    hipStream_t lane1_stream = nullptr;  // lane 1's stream (lane 0 runs on `stream`)
+    int next_lane = 0;
 
     // scratch for the per-stage entry points (grow-only)
     void *scr[4] = {};
@@ -188,6 +196,8 @@ struct tpmd_ctx {
 
     ~tpmd_ctx() {
         if (device >= 0) (void) hipSetDevice(device);
+        if (lane1_stream) (void) hipStreamSynchronize(lane1_stream);
+        if (own_stream) (void) hipStreamSynchronize(own_stream);
         for (auto e : ev) (void) hipEventDestroy(e);
         for (void *p : allocs) (void) hipFree(p);
         for (void *p : batch_allocs) (void) hipFree(p);
@@ -201,6 +211,7 @@ struct tpmd_ctx {
         }
         if (fs.copy) (void) hipStreamDestroy(fs.copy);
         if (own_stream) (void) hipStreamDestroy(own_stream);
+        if (lane1_stream) (void) hipStreamDestroy(lane1_stream);
     }
 };
 
@@ -359,6 +370,12 @@ bool check_ctx(tpmd_ctx *c) {
 // their epilogue (the stage output never goes to HBM)
 bool fused_tail(const tpmd_ctx *c, int oc, int r) { return modconv_fusable(oc, r, c->f16); }
 
+// work of the other lane finished (before anything that rewrites shared
+// state or hands results back through lane 0 alone)
+bool drain_lanes(tpmd_ctx *c) {
+    return !c->lane1_stream || c->hip_ok(hipStreamSynchronize(c->lane1_stream), "lane sync");
+}
+
 // stage entry points run on the caller's stream; NULL is HIP's null stream
 hipStream_t pick_stream(tpmd_ctx *, void *s) { return (hipStream_t) s; }
 
@@ -414,7 +431,8 @@ tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *st
         }
     }
     c->tensors = tensor_list(c);
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->lane1_stream, hipStreamNonBlocking) != hipSuccess) {
         fprintf(stderr, "tpmd_create: stream creation failed\n");
         delete c;
         return nullptr;
@@ -476,6 +494,7 @@ const char *tpmd_weight_name(const tpmd_ctx *c, int i, int64_t *n, int *is_matri
 
 int tpmd_prepare(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
+    if (!drain_lanes(c)) return -1;
     for (void *p : c->allocs) (void) hipFree(p);
     c->allocs.clear();
     c->prepared = false;
@@ -579,6 +598,7 @@ int tpmd_prepare(tpmd_ctx *c) {
 
 int tpmd_build(tpmd_ctx *c, int max_batch) {
     if (!check_ctx(c)) return -1;
+    if (!drain_lanes(c)) return -1;
     if (!c->prepared) {
         c->err = "decoder not prepared";
         return -1;
@@ -644,24 +664,27 @@ int tpmd_build(tpmd_ctx *c, int max_batch) {
     }
     const size_t R = (size_t) c->out_res();
     auto A = [&](size_t bytes) { return c->dalloc(bytes, c->batch_allocs); };
-    c->lat = (float *) A((size_t) B * 512 * 4);
-    c->s_all = (float *) A((size_t) s_total * 4);
-    c->den_all = (float *) A((size_t) doff * 4);
-    c->xs0 = A((size_t) B * 16 * C0 * c->act_size());
-    c->c1 = A((size_t) B * act_max * c->act_size());
-    c->trunk = A((size_t) B * act_max * c->act_size());
-    c->outb = (float *) A((size_t) B * std::max<size_t>(out_max, 1) * 4);
-    c->ws_elems = ws_max;
-    c->ws = ws_max > 0 ? (float *) A((size_t) ws_max * 4) : nullptr;
-    if (ws_max > 0 && !c->ws) return -1;
+    for (int li = 1; li >= 0; li--) {
+    c->L = &c->lane[li];
+    c->L->lat = (float *) A((size_t) B * 512 * 4);
+    c->L->s_all = (float *) A((size_t) s_total * 4);
+    c->L->den_all = (float *) A((size_t) doff * 4);
+    c->L->xs0 = A((size_t) B * 16 * C0 * c->act_size());
+    c->L->c1 = A((size_t) B * act_max * c->act_size());
+    c->L->trunk = A((size_t) B * act_max * c->act_size());
+    c->L->outb = (float *) A((size_t) B * std::max<size_t>(out_max, 1) * 4);
+    c->L->ws_elems = ws_max;
+    c->L->ws = ws_max > 0 ? (float *) A((size_t) ws_max * 4) : nullptr;
+    if (ws_max > 0 && !c->L->ws) return -1;
     for (int i = 0; i < 2; i++) {
-        c->flow[i] = (float *) A((size_t) B * skip_max * 4);
-        c->rgb[i] = (float *) A((size_t) B * skip_max * 4);
+        c->L->flow[i] = (float *) A((size_t) B * skip_max * 4);
+        c->L->rgb[i] = (float *) A((size_t) B * skip_max * 4);
     }
-    c->img = (float *) A((size_t) B * 3 * R * R * 4);
-    if (!c->lat || !c->s_all || !c->den_all || !c->xs0 || !c->c1 || !c->trunk || !c->outb ||
-        !c->flow[0] || !c->flow[1] || !c->rgb[0] || !c->rgb[1] || !c->img)
+    c->L->img = (float *) A((size_t) B * 3 * R * R * 4);
+    if (!c->L->lat || !c->L->s_all || !c->L->den_all || !c->L->xs0 || !c->L->c1 || !c->L->trunk || !c->L->outb ||
+        !c->L->flow[0] || !c->L->flow[1] || !c->L->rgb[0] || !c->L->rgb[1] || !c->L->img)
         return -1;
+    }  // lanes; c->L is lane 0 again
     for (int j = 0; j < ns; j++) {
         const size_t r = (size_t) 8 << j;
         const size_t fb = r * r * c->oc[j] * c->act_size() + TAIL_FEAT_PAD;  // + zero pad
@@ -682,6 +705,7 @@ int tpmd_out_res(const tpmd_ctx *c) { return c ? c->out_res() : 0; }
 
 static int set_feats_impl(tpmd_ctx *c, const float *const *feats, bool dev) {
     if (!check_ctx(c)) return -1;
+    if (!drain_lanes(c)) return -1;
     if (!c->built) {
         c->err = "decoder not built";
         return -1;
@@ -721,23 +745,23 @@ static TailArgs stage_tail_args(tpmd_ctx *c, int j, int n, float *img_dst) {
     const StageW &s = c->st[j];
     const bool last = j + 1 == c->ns;
     TailArgs a{};
-    a.out = c->outb;
+    a.out = c->L->outb;
     a.feat = s.feat;
     a.wflow = s.wflow;
-    a.sflow = c->s_all + s.s_off;
+    a.sflow = c->L->s_all + s.s_off;
     a.fbias = s.fbias;
     a.fup = s.fup;
-    a.flow_prev = j > 0 ? c->flow[(j - 1) & 1] : nullptr;
-    a.flow_cur = last ? nullptr : c->flow[j & 1];
+    a.flow_prev = j > 0 ? c->L->flow[(j - 1) & 1] : nullptr;
+    a.flow_cur = last ? nullptr : c->L->flow[j & 1];
     a.lin = s.lin;
     a.wrgb = s.wrgb;
     a.rlb = s.rlb;
     a.rbias = s.rbias;
     a.rup = s.rup;
-    a.rgb_prev = j > 0 ? c->rgb[(j - 1) & 1] : nullptr;
-    a.rgb_cur = last ? img_dst : c->rgb[j & 1];
-    a.s_next = last ? nullptr : c->s_all + c->conv[3 + 2 * j].s_off;
-    a.trunk = last ? nullptr : c->trunk;
+    a.rgb_prev = j > 0 ? c->L->rgb[(j - 1) & 1] : nullptr;
+    a.rgb_cur = last ? img_dst : c->L->rgb[j & 1];
+    a.s_next = last ? nullptr : c->L->s_all + c->conv[3 + 2 * j].s_off;
+    a.trunk = last ? nullptr : c->L->trunk;
     a.warp_tap = nullptr;
     a.featg = a.trunk ? nullptr : s.featg;
     a.nframes = n;
@@ -756,7 +780,7 @@ static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void
     a.A_chunk = cv.A_chunk;
     a.X = X;
     a.Y = Y;
-    a.inv_den = c->den_all + cv.d_off;
+    a.inv_den = c->L->den_all + cv.d_off;
     a.bias = cv.bias;
     a.out_scale = out_scale;
     a.nframes = n;
@@ -765,8 +789,8 @@ static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void
     a.IC = cv.ic;
     a.OC = cv.oc;
     a.x_bstride = (int64_t) H * H * cv.ic;
-    a.ws = c->ws;
-    a.ws_elems = c->ws_elems;
+    a.ws = c->L->ws;
+    a.ws_elems = c->L->ws_elems;
     return a;
 }
 
@@ -779,32 +803,32 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
         if (c->profile) (void) hipEventRecord(c->ev[(size_t) slot++], st);
     };
     mark();
-    if (!c->hip_ok(launch_style_gemv(c->wmod, c->bmod, c->lat, c->s_all, c->seg, n, st), "style")) return false;
-    if (!c->hip_ok(launch_demod(c->saug_all, c->s_all, c->den_all, c->dem, n, st), "demod")) return false;
+    if (!c->hip_ok(launch_style_gemv(c->wmod, c->bmod, c->L->lat, c->L->s_all, c->seg, n, st), "style")) return false;
+    if (!c->hip_ok(launch_demod(c->saug_all, c->L->s_all, c->L->den_all, c->dem, n, st), "demod")) return false;
     const ConvW &k1 = c->conv[0];
-    if (!c->hip_ok(launch_prescale_input(f16, c->input_cl, c->s_all + k1.s_off, c->xs0, C0, n, st), "prescale"))
+    if (!c->hip_ok(launch_prescale_input(f16, c->input_cl, c->L->s_all + k1.s_off, c->L->xs0, C0, n, st), "prescale"))
         return false;
     // conv1 -> trunk (pre-scaled by the stage-0 up-conv style)
-    if (!c->hip_ok(launch_modconv(conv_args(c, k1, n, 4, c->xs0, c->trunk, c->s_all + c->conv[1].s_off, f16), st),
+    if (!c->hip_ok(launch_modconv(conv_args(c, k1, n, 4, c->L->xs0, c->L->trunk, c->L->s_all + c->conv[1].s_off, f16), st),
                    "conv1"))
         return false;
     for (int j = 0; j < ns; j++) {
         const int r = 8 << j, rh = r / 2, C = c->oc[j];
         const ConvW &up = c->conv[1 + 2 * j], &dn = c->conv[2 + 2 * j];
         mark();
-        if (!c->hip_ok(launch_modconv(conv_args(c, up, n, rh, c->trunk, c->c1, c->s_all + dn.s_off, f16), st),
+        if (!c->hip_ok(launch_modconv(conv_args(c, up, n, rh, c->L->trunk, c->L->c1, c->L->s_all + dn.s_off, f16), st),
                        "up-conv"))
             return false;
         mark();
         const TailArgs ta = stage_tail_args(c, j, n, img_dst);
         if (fused_tail(c, C, r)) {
-            ConvArgs ca = conv_args(c, dn, n, r, c->c1, nullptr, nullptr, false);
+            ConvArgs ca = conv_args(c, dn, n, r, c->L->c1, nullptr, nullptr, false);
             ca.tail = &ta;
             ca.trunk_f16 = f16;
             if (!c->hip_ok(launch_modconv(ca, st), "conv+tail")) return false;
             mark();
         } else {
-            if (!c->hip_ok(launch_modconv(conv_args(c, dn, n, r, c->c1, c->outb, nullptr, false), st), "conv"))
+            if (!c->hip_ok(launch_modconv(conv_args(c, dn, n, r, c->L->c1, c->L->outb, nullptr, false), st), "conv"))
                 return false;
             mark();
             if (!c->hip_ok(launch_stage_tail(ta, f16, false, f16, st), "tail")) return false;
@@ -814,8 +838,30 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
     return true;
 }
 
+static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device);
+
 int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
     if (!check_ctx(c)) return -1;
+    // device-resident decodes on the library's own stream alternate lanes;
+    // every other form (host buffers, a caller's stream, per-stage
+    // profiling) runs on lane 0 after the other lane has drained
+    const bool two = on_device && imgs && !c->profile && c->stream == c->own_stream && c->lane1_stream;
+    if (!two) {
+        if (!drain_lanes(c)) return -1;
+        return decode_batch_lane(c, styles, n, imgs, on_device);
+    }
+    const int k = c->next_lane;
+    c->next_lane ^= 1;
+    hipStream_t keep = c->stream;
+    c->L = &c->lane[k];
+    if (k == 1) c->stream = c->lane1_stream;
+    const int rc = decode_batch_lane(c, styles, n, imgs, on_device);
+    c->L = &c->lane[0];
+    c->stream = keep;
+    return rc;
+}
+
+static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
     if (!c->built) {
         c->err = "decoder not built";
         return -1;
@@ -830,7 +876,7 @@ int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int 
     }
     const size_t R = (size_t) c->out_res();
     const hipMemcpyKind k_in = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-    if (!c->hip_ok(hipMemcpyAsync(c->lat, styles, (size_t) n * 512 * 4, k_in, c->stream), "style upload"))
+    if (!c->hip_ok(hipMemcpyAsync(c->L->lat, styles, (size_t) n * 512 * 4, k_in, c->stream), "style upload"))
         return -1;
     if (c->profile) {
         const size_t need = (size_t) 2 + 3 * c->ns;
@@ -840,10 +886,10 @@ int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int 
             c->ev.push_back(e);
         }
     }
-    float *dst = (on_device && imgs) ? imgs : c->img;
+    float *dst = (on_device && imgs) ? imgs : c->L->img;
     if (!enqueue_decode(c, n, dst)) return -1;
     if (!on_device) {
-        if (imgs && !c->hip_ok(hipMemcpyAsync(imgs, c->img, (size_t) n * 3 * R * R * 4, hipMemcpyDeviceToHost,
+        if (imgs && !c->hip_ok(hipMemcpyAsync(imgs, c->L->img, (size_t) n * 3 * R * R * 4, hipMemcpyDeviceToHost,
                                               c->stream), "image download"))
             return -1;
         if (!c->hip_ok(hipStreamSynchronize(c->stream), "decode")) return -1;
@@ -890,6 +936,7 @@ static bool frame_slots(tpmd_ctx *c, size_t bytes) {
 int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, int format, void *out,
                            tpmd_frame_cb cb, void *ud) {
     if (!check_ctx(c)) return -1;
+    if (!drain_lanes(c)) return -1;
     if (!c->built || !c->feats_set) {
         c->err = !c->built ? "decoder not built" : "feats not set";
         return -1;
@@ -926,14 +973,14 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
         const int nk = (int) std::min<int64_t>(B, n_frames - t0);
         // slot s is free once the copy of batch k-2 has finished
         if (k >= 2 && !c->hip_ok(hipStreamWaitEvent(c->stream, f.copied[s], 0), "wait")) ok = false;
-        ok = ok && c->hip_ok(hipMemcpyAsync(c->lat, styles + (size_t) t0 * 512, (size_t) nk * 512 * 4,
+        ok = ok && c->hip_ok(hipMemcpyAsync(c->L->lat, styles + (size_t) t0 * 512, (size_t) nk * 512 * 4,
                                             hipMemcpyHostToDevice, c->stream),
                              "style upload");
         if (format == TPMD_FRAME_F32) {
             ok = ok && enqueue_decode(c, nk, (float *) f.dev[s]);
         } else {
-            ok = ok && enqueue_decode(c, nk, c->img) &&
-                 c->hip_ok(launch_rgb24(c->img, nk, (int) R, (uint8_t *) f.dev[s], c->stream), "rgb24");
+            ok = ok && enqueue_decode(c, nk, c->L->img) &&
+                 c->hip_ok(launch_rgb24(c->L->img, nk, (int) R, (uint8_t *) f.dev[s], c->stream), "rgb24");
         }
         ok = ok && c->hip_ok(hipEventRecord(f.computed[s], c->stream), "event") &&
              c->hip_ok(hipStreamWaitEvent(f.copy, f.computed[s], 0), "wait") &&
@@ -956,13 +1003,14 @@ int tpmd_decode(tpmd_ctx *c, const float *style, float *img) {
 
 int tpmd_set_stream(tpmd_ctx *c, void *stream) {
     if (!check_ctx(c)) return -1;
+    if (!drain_lanes(c)) return -1;
     c->stream = (hipStream_t) stream;
     return 0;
 }
 
 int tpmd_sync(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
-    return c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
+    return drain_lanes(c) && c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
 }
 
 int tpmd_profile_stages(tpmd_ctx *c, int enable) {

@@ -71,6 +71,23 @@ def test_decode_paths_agree(om, torch_cuda):
     assert np.array_equal(out.cpu().numpy(), full)
 
 
+def test_two_lane_device_decodes(om, torch_cuda):
+    """device decodes on the library's own stream alternate between two
+    lanes (consecutive batches overlap on the GPU): every batch equals the
+    host path bit for bit, the ragged last one included"""
+    torch = torch_cuda
+    _, dec, lat = _decoders(om, "f16", SMALL_IC, SMALL_OC, 7, 2)
+    starts = range(0, 7, 2)
+    want = np.concatenate([dec.decode_batch(lat[t:t + 2]) for t in starts])
+    sd = torch.from_numpy(lat).cuda()
+    outs = [torch.empty((min(2, 7 - t), 3, 512, 512), device="cuda") for t in starts]
+    torch.cuda.synchronize()             # inputs ready before the decoder's streams read them
+    for o, t in zip(outs, starts):
+        dec.decode_batch_device(sd[t:t + 2], o)
+    dec.sync()
+    assert np.array_equal(np.concatenate([o.cpu().numpy() for o in outs]), want)
+
+
 def test_error_contract(torch_cuda):
     dec = tpmd.MotionDecoder("f32", 2, (64, 64), (64, 64))
     with pytest.raises(tpmd.TpmdError, match="decoder not prepared"):
