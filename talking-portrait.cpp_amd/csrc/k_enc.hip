@@ -66,6 +66,32 @@ __global__ __launch_bounds__(256) void enc_blur_kernel(const float *__restrict__
     }
 }
 
+// bias, activation, gate, residual; f32 store and operand-type copy of 4
+// consecutive outputs o..o+3 of pixel n
+__device__ __forceinline__ void enc_epilogue(const EncConvParams &p, int n, int o, const float acc[4]) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float a = acc[j];
+        if (p.bias) a = a + p.bias[o + j];
+        if (p.leaky == 1) a = leaky(a);
+        else if (p.leaky == 2) a = gelu_tanh(a);
+        if (p.gate) a = p.gate[(int64_t) n * p.gstride + o + j] * a;
+        v[j] = a;
+    }
+    const int64_t off = (int64_t) n * p.OC + o;
+    if (p.res) {
+        const floatx4 r = *(const floatx4 *) (p.res + off);
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = r[j] + v[j];
+    }
+    if (p.Y) *(floatx4 *) (p.Y + off) = floatx4{v[0], v[1], v[2], v[3]};
+    if (p.Ya) {
+        if (p.ya_f16) store4<half_t>((half_t *) p.Ya + off, v[0], v[1], v[2], v[3]);
+        else store4<float>((float *) p.Ya + off, v[0], v[1], v[2], v[3]);
+    }
+}
+
 // 64 output channels x 64 output pixels per workgroup, k tiles of 32 input
 // channels of one tap; 4 waves of 32 x 32 (one 32x32 MFMA accumulator each);
 // operand rows in LDS padded by 16 bytes (conflict-free fragment reads); the
@@ -88,7 +114,9 @@ __global__ __launch_bounds__(256) void enc_conv_kernel(EncConvParams p) {
     const int IC = p.IC, OC = p.OC, N = p.OH * p.OW;
     const int K = p.KH * p.KW * IC;
     const int cpt = IC / BK;                        // k tiles per tap
-    const int T = p.KH * p.KW * cpt;
+    const int TT = p.KH * p.KW * cpt;
+    const int ks_n = p.ksplit > 1 ? p.ksplit : 1, split = (int) blockIdx.z;
+    const int t_begin = (int) ((int64_t) split * TT / ks_n), t_end = (int) ((int64_t) (split + 1) * TT / ks_n);
     const TA *A = (const TA *) p.A, *X = (const TA *) p.X;
 
     // this thread's chunks: chunk u = tid + i*256 -> row u / CH, chunk u % CH
@@ -135,12 +163,12 @@ __global__ __launch_bounds__(256) void enc_conv_kernel(EncConvParams p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.0f;
     const int lrow = lane & 31, khalf = lane >> 5;
-    load(0);
+    load(t_begin);
     store(0);
     __syncthreads();
-    for (int t = 0; t < T; t++) {
-        const int s = t & 1;
-        if (t + 1 < T) load(t + 1);
+    for (int t = t_begin; t < t_end; t++) {
+        const int s = (t - t_begin) & 1;
+        if (t + 1 < t_end) load(t + 1);
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const int kc = ks * 2 + khalf;
@@ -148,7 +176,7 @@ __global__ __launch_bounds__(256) void enc_conv_kernel(EncConvParams p) {
             const u32x4 bf = *(const u32x4 *) (Bs[s] + (wn * 32 + lrow) * RS + kc * 16);
             mfma_op<TA>::run(af, bf, acc);
         }
-        if (t + 1 < T) {
+        if (t + 1 < t_end) {
             store(s ^ 1);
             __syncthreads();
         }
@@ -161,27 +189,26 @@ __global__ __launch_bounds__(256) void enc_conv_kernel(EncConvParams p) {
     for (int i = 0; i < 4; i++) {
         const int o = m0 + wm * 32 + i * 8 + khalf * 4;
         if (o >= OC) continue;
-        float v[4];
+        const float q[4] = {acc[i * 4], acc[i * 4 + 1], acc[i * 4 + 2], acc[i * 4 + 3]};
+        if (ks_n > 1) *(floatx4 *) (p.ws + ((int64_t) split * N + n) * OC + o) = floatx4{q[0], q[1], q[2], q[3]};
+        else enc_epilogue(p, n, o, q);
+    }
+}
+
+// split-K second pass: the partials summed in split order, then the epilogue
+__global__ __launch_bounds__(256) void enc_splitk_kernel(EncConvParams p) {
+    const int N = p.OH * p.OW, OQ = p.OC / 4;
+    const int64_t total = (int64_t) N * OQ;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        const int n = (int) (i / OQ), o = (int) (i - (int64_t) n * OQ) * 4;
+        floatx4 a = *(const floatx4 *) (p.ws + (int64_t) n * p.OC + o);
+        for (int s = 1; s < p.ksplit; s++) {
+            const floatx4 b = *(const floatx4 *) (p.ws + ((int64_t) s * N + n) * p.OC + o);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float a = acc[i * 4 + j];
-            if (p.bias) a = a + p.bias[o + j];
-            if (p.leaky == 1) a = leaky(a);
-            else if (p.leaky == 2) a = gelu_tanh(a);
-            if (p.gate) a = p.gate[(int64_t) n * p.gstride + o + j] * a;
-            v[j] = a;
+            for (int j = 0; j < 4; j++) a[j] = a[j] + b[j];
         }
-        const int64_t off = (int64_t) n * OC + o;
-        if (p.res) {
-            const floatx4 r = *(const floatx4 *) (p.res + off);
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = r[j] + v[j];
-        }
-        if (p.Y) *(floatx4 *) (p.Y + off) = floatx4{v[0], v[1], v[2], v[3]};
-        if (p.Ya) {
-            if (p.ya_f16) store4<half_t>((half_t *) p.Ya + off, v[0], v[1], v[2], v[3]);
-            else store4<float>((float *) p.Ya + off, v[0], v[1], v[2], v[3]);
-        }
+        const float q[4] = {a[0], a[1], a[2], a[3]};
+        enc_epilogue(p, n, o, q);
     }
 }
 
@@ -236,9 +263,18 @@ hipError_t launch_enc_blur(const float *x, const float *k, int H, int W, int C, 
 
 hipError_t launch_enc_conv(EncConvParams p, bool f16, hipStream_t st) {
     if (p.IC % 32 != 0 || p.OC % 4 != 0 || p.OH < 1 || p.OW < 1) return hipErrorInvalidValue;
-    dim3 grid((unsigned) ((p.OH * p.OW + 63) / 64), (unsigned) ((p.OC + 63) / 64));
+    const int T = p.KH * p.KW * p.IC / 32;
+    if (p.ksplit < 1) p.ksplit = 1;
+    if (p.ksplit > T || (p.ksplit > 1 && !p.ws)) return hipErrorInvalidValue;
+    dim3 grid((unsigned) ((p.OH * p.OW + 63) / 64), (unsigned) ((p.OC + 63) / 64), (unsigned) p.ksplit);
     if (f16) hipLaunchKernelGGL(enc_conv_kernel<half_t>, grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL(enc_conv_kernel<float>, grid, dim3(256), 0, st, p);
+    if (p.ksplit > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(enc_splitk_kernel, dim3(grid_1d((int64_t) p.OH * p.OW * (p.OC / 4))), dim3(256), 0, st,
+                           p);
+    }
     return hipGetLastError();
 }
 

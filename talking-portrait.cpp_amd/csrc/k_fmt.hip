@@ -3,6 +3,7 @@
 // row of tokens):
 //
 //   fmt_convert_kernel   f32 rows -> GEMM operand type, zero-padding K
+//   fmt_tfreq_kernel     the GLIDE timestep features
 //   fmt_silu_kernel      in place, the t-embedder's hidden layer
 //   fmt_cond_kernel      silu(c_embed + t_embed) in the adaLN GEMMs' operand type
 //   fmt_xpos_kernel      x = x_embed + pos, replicated over the CFG branches
@@ -28,6 +29,17 @@ __global__ __launch_bounds__(256) void fmt_convert_kernel(const float *__restric
         const int64_t r = i / ld;
         const int c = (int) (i - r * ld);
         y[i] = fmt_cast<TO>(c < cols ? x[r * cols + c] : 0.0f);
+    }
+}
+
+// [cos(t f_k), sin(t f_k)], k < half (the product rounded to f32 first, as the reference)
+__global__ __launch_bounds__(256) void fmt_tfreq_kernel(const float *__restrict__ fk, float t, int half,
+                                                        float *__restrict__ y) {
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k < half) {
+        const float a = t * fk[k];
+        y[k] = cosf(a);
+        y[half + k] = sinf(a);
     }
 }
 
@@ -185,6 +197,11 @@ hipError_t launch_fmt_convert(const float *x, int rows, int cols, int ld, void *
     const unsigned g = fmt_grid((int64_t) rows * ld);
     if (f16) hipLaunchKernelGGL(fmt_convert_kernel<half_t>, dim3(g), dim3(256), 0, st, x, rows, cols, ld, (half_t *) y);
     else hipLaunchKernelGGL(fmt_convert_kernel<float>, dim3(g), dim3(256), 0, st, x, rows, cols, ld, (float *) y);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_tfreq(const float *fk, float t, int half, float *y, hipStream_t st) {
+    hipLaunchKernelGGL(fmt_tfreq_kernel, dim3((unsigned) ((half + 255) / 256)), dim3(256), 0, st, fk, t, half, y);
     return hipGetLastError();
 }
 

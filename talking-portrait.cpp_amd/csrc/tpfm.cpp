@@ -37,6 +37,15 @@ struct FTensor {
 
 int round32(int v) { return (v + 31) / 32 * 32; }
 
+// split-K factor of a linear layer over `rows` tokens: about 1024
+// workgroups (the GEMM's 64 x 64 tiles are few at 180 rows, and a short k
+// loop per workgroup hides the load latency), at least 2 k tiles each
+int lin_splits(int rows, int out, int in) {
+    const int tiles = ((rows + 63) / 64) * ((out + 63) / 64);
+    const int T = in / 32;
+    return std::max(1, std::min(1024 / std::max(tiles, 1), T / 2));
+}
+
 }  // namespace
 
 struct tpfm_ctx {
@@ -68,9 +77,10 @@ struct tpfm_ctx {
     std::vector<float> t_freqs;
 
     // activations
-    float *tf = nullptr, *te0 = nullptr, *te = nullptr;
+    float *tfk = nullptr, *tf = nullptr, *te0 = nullptr, *te = nullptr;
     float *cond_f = nullptr, *clin = nullptr, *x60 = nullptr, *x1 = nullptr, *x = nullptr;
     float *mod = nullptr, *qkv = nullptr, *fmod = nullptr, *v = nullptr;
+    float *ws = nullptr;  // split-K partials
     void *cond_a = nullptr, *sc_a = nullptr, *x60_a = nullptr, *h_a = nullptr, *o_a = nullptr, *m1_a = nullptr;
 
     bool hip_ok(hipError_t e, const char *what) {
@@ -210,6 +220,8 @@ bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float 
     p.pad = 0;
     p.OH = 1;
     p.OW = rows;
+    p.ksplit = lin_splits(rows, L.out, L.in);
+    p.ws = c->ws;
     return c->hip_ok(launch_enc_conv(p, L.f16, c->stream), "linear");
 }
 
@@ -219,21 +231,13 @@ bool enqueue_forward(tpfm_ctx *c, float t) {
     const tpfm_config &g = c->cfg;
     const int H = g.dim_h, T = c->T, R = c->B * T;
     hipStream_t st = c->stream;
-    // t embedding: GLIDE features on the host (src/fmt.cpp:168-174), two GEMVs
-    const int half = g.t_freq_dim / 2;
-    std::vector<float> tf((size_t) g.t_freq_dim);
-    for (int k = 0; k < half; k++) {
-        const float a = t * c->t_freqs[(size_t) k];
-        tf[(size_t) k] = cosf(a);
-        tf[(size_t) (half + k)] = sinf(a);
-    }
-    if (!c->hip_ok(hipMemcpyAsync(c->tf, tf.data(), tf.size() * 4, hipMemcpyHostToDevice, st), "t_freq")) return false;
-    if (!c->hip_ok(launch_enc_linear(c->t0w, c->t0b, c->tf, H, g.t_freq_dim, c->t0_16, c->te0, st), "t_embed") ||
+    // t embedding: GLIDE features cos / sin(t f_k) (src/fmt.cpp:168-174, the
+    // f_k table made on the host as there), two GEMVs
+    if (!c->hip_ok(launch_fmt_tfreq(c->tfk, t, g.t_freq_dim / 2, c->tf, st), "t_freq") ||
+        !c->hip_ok(launch_enc_linear(c->t0w, c->t0b, c->tf, H, g.t_freq_dim, c->t0_16, c->te0, st), "t_embed") ||
         !c->hip_ok(launch_fmt_silu(c->te0, H, st), "silu") ||
         !c->hip_ok(launch_enc_linear(c->t2w, c->t2b, c->te0, H, H, c->t2_16, c->te, st), "t_embed"))
         return false;
-    // the tf staging vector must outlive the copy
-    if (!c->hip_ok(hipStreamSynchronize(st), "t_freq sync")) return false;
     // c = c_embed(cond) + t_emb; the adaLN layers read silu(c)
     const bool sc16 = c->blocks.empty() ? c->fin_mod.f16 : c->blocks[0].mod.f16;
     if (!linear(c, c->cemb, c->cond_a, R, c->clin, nullptr, false, 0) ||
@@ -416,6 +420,7 @@ int tpfm_prepare(tpfm_ctx *c) {
     auto F = [&](size_t n) { return (float *) c->dalloc(n * 4); };
     auto A = [&](size_t n) { return c->dalloc(n * 4); };  // operand buffers sized for f32
     c->tf = F((size_t) g.t_freq_dim);
+    c->tfk = c->upload(c->t_freqs);
     c->te0 = F((size_t) H);
     c->te = F((size_t) H);
     c->cond_f = F((size_t) R * c->CD);
@@ -433,8 +438,27 @@ int tpfm_prepare(tpfm_ctx *c) {
     c->m1_a = A((size_t) R * c->MLP);
     c->fmod = F((size_t) R * 2 * H);
     c->v = F((size_t) R * g.dim_w);
-    if (!c->tf || !c->te0 || !c->te || !c->cond_f || !c->cond_a || !c->clin || !c->sc_a || !c->x60 || !c->x60_a ||
-        !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->fmod || !c->v)
+    {
+        size_t wsn = 1;
+        auto need_ws = [&](const tpfm_ctx::Lin &L, int rows) {
+            const int k = lin_splits(rows, L.out, L.in);
+            if (k > 1) wsn = std::max(wsn, (size_t) k * rows * L.out);
+        };
+        need_ws(c->cemb, R);
+        need_ws(c->xemb, T);
+        need_ws(c->fin_mod, R);
+        need_ws(c->fin_lin, R);
+        for (const auto &B : c->blocks) {
+            need_ws(B.mod, R);
+            need_ws(B.qkv, R);
+            need_ws(B.proj, R);
+            need_ws(B.fc1, R);
+            need_ws(B.fc2, R);
+        }
+        c->ws = F(wsn);
+    }
+    if (!c->tf || !c->tfk || !c->te0 || !c->te || !c->cond_f || !c->cond_a || !c->clin || !c->sc_a || !c->x60 || !c->x60_a ||
+        !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->fmod || !c->v || !c->ws)
         return -1;
     c->prepared = true;
     return 0;

@@ -20,6 +20,8 @@ struct EncConvParams {
     int leaky;              // activation after the bias: 0 none, 1 leaky_relu 0.2, 2 tanh-GELU
     const float *gate;      // gate[n * gstride + o] multiplies the activation, or null
     int64_t gstride;
+    int ksplit;             // > 1: k split over gridDim.z, partials in ws, epilogue in a second pass
+    float *ws;              // [ksplit][OH*OW][OC] f32 (ksplit > 1)
     int H, W, IC, OC, KH, KW, stride, pad, OH, OW;
 };
 

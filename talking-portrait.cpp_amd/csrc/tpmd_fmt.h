@@ -10,6 +10,7 @@
 namespace tpmd {
 
 hipError_t launch_fmt_convert(const float *x, int rows, int cols, int ld, void *y, bool f16, hipStream_t st);
+hipError_t launch_fmt_tfreq(const float *fk, float t, int half, float *y, hipStream_t st);
 hipError_t launch_fmt_silu(float *x, int n, hipStream_t st);
 hipError_t launch_fmt_cond(const float *clin, const float *temb, int rows, int H, void *y, bool f16, hipStream_t st);
 hipError_t launch_fmt_xpos(const float *x1, const float *pos, int T, int H, int B, float *x, hipStream_t st);
