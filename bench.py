@@ -220,6 +220,8 @@ def main():
     ap.add_argument("--ftype", default="f16", choices=["f16", "f32"])
     ap.add_argument("--workload", default="iid", choices=["iid", "smooth", "stress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lanes", type=int, default=2, choices=[1, 2],
+                    help="1: every launch chain on one stream (kernel traces comparable with the per-stage events)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run the 256 MiB calibration copy (for counter runs)")
     args = ap.parse_args()
@@ -245,6 +247,8 @@ def main():
     lat_dev = torch.from_numpy(np.concatenate([lat, lat[:B]])).cuda()   # wrap-around window
     imgs = torch.empty((B, 3, 512, 512), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()   # inputs resident before the decoder stream reads them
+    if args.lanes == 1:
+        dec.use_stream(torch.cuda.current_stream())   # a caller's stream: one lane
 
     def step(k):
         t0 = (k * B) % n_seq
@@ -299,6 +303,7 @@ def main():
         "roofline": r,
         "stages": stages,
         "stage_sum_us": round(float(us.sum()), 1),
+        "lanes": args.lanes,
     }
     # the clip delivered to host memory through the frame output path
     # (downloads overlapped with decoding): reported beside `value`, never as it
