@@ -188,6 +188,69 @@ def fmt_timing(ftype, reps=5):
             "note": "tpfm_forward / tpfm_sample_chunk, host buffers, synchronous (host clock)"}
 
 
+def gather_timing(reps=50):
+    """the standalone bilinear gather (tpmd_gather, GGML_OP_BILINEAR_GATHER)
+    on device buffers, HIP events on the stream it runs on.  Algorithmic bytes
+    per launch: N * 8 (grid) + the feature map once + N * C * 4 (f32 output).
+    Grids: i.i.d. U(-a, a) (random taps, the single-stage and stress
+    workloads) or a warp (pixel centres plus a smooth displacement of a few
+    pixels and sub-pixel jitter, what the decoder's flow heads produce).
+    The launches are replayed from a HIP graph; the graph holds kernel nodes
+    only."""
+    import torch
+    import tpmd
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(1003)
+    rows = []
+    for C, R, nf, f16, kind in ((512, 64, 1, False, 1.1), (512, 64, 16, False, 1.1), (512, 64, 16, True, 2.0),
+                                (512, 64, 16, True, "warp"), (128, 128, 16, True, "warp"),
+                                (64, 256, 16, True, "warp"), (32, 512, 16, True, "warp")):
+        N = nf * R * R
+        feat = torch.randn(R * R, C, device=dev, generator=g)
+        feat = feat.half() if f16 else feat
+        if kind == "warp":
+            ax = (2 * torch.arange(R, device=dev, dtype=torch.float32) + 1) / R - 1
+            gy, gx = torch.meshgrid(ax, ax, indexing="ij")
+            jit = (torch.rand(nf, R, R, 2, device=dev, generator=g) - 0.5) / R
+            grid = torch.stack([gx + 0.05 * torch.sin(3 * gy), gy + 0.05 * torch.cos(2 * gx)], -1) + jit
+            grid = grid.reshape(N, 2).contiguous()
+        else:
+            grid = (torch.rand(N, 2, device=dev, generator=g) * 2 - 1) * kind
+        ref = tpmd.gather(feat, R, R, grid)
+        out = torch.empty(N, C, device=dev)
+        # the reps captured in one HIP graph: back-to-back launches, so the
+        # events time the kernels, not the host's per-call launch cost
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                tpmd.gather(feat, R, R, grid, out=out)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                tpmd.gather(feat, R, R, grid, out=out)
+        graph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        same = bool(torch.equal(out, ref))   # the replayed launches reproduce the eager one bit for bit
+        del graph
+        nbytes = N * 8 + R * R * C * feat.element_size() + N * C * 4
+        name = (f"{C}x{R}x{R} {'f16' if f16 else 'f32'} feat, {nf} frame(s), "
+                + ("warp grid" if kind == "warp" else f"grid U(-{kind}, {kind})"))
+        row = roofline(name, 0, nbytes, us, "f16")
+        row["mb"] = round(nbytes / 1e6, 2)
+        row["replay_matches_eager"] = same
+        rows.append(row)
+        del feat, grid, out, ref
+    return rows
+
+
 def cpu_baseline(ftype_unused=None):
     """the CPU oracle's fast graph (f32, numpy/OpenBLAS + OpenMP C ops) on
     this host, one 512x512 frame"""
@@ -317,6 +380,7 @@ def main():
                                  "note": "pageable host buffer, PCIe download included"}
     out["encoder"] = encoder_timing(args.ftype)
     out["fmt"] = fmt_timing(args.ftype)
+    out["gather"] = gather_timing()
     if args.copy_probe:
         copy_probe()
     if not args.no_cpu_baseline:

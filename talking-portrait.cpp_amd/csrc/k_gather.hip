@@ -12,52 +12,104 @@ namespace tpmd {
 
 // ---------------------------------------------------------------------------
 // CL gather, vectorised: G lanes share one grid point and split its C
-// channels in 16-byte chunks (CPL chunks per lane, C = G * CPL * VEC).  All
-// lanes of a group read the same tap rows, so a wave reads whole contiguous
-// channel runs of the feature map (coalesced) and writes a contiguous
-// [C] output row per point.
-template <typename TF, int G, int CPL>
-__global__ __launch_bounds__(256) void gather_cl_vec(const TF *__restrict__ feat,
+// channels in chunks of V = 4 elements (16 bytes f32, 8 bytes f16; CPL chunks
+// per lane, C = G * CPL * 4).  All lanes of a group read the same tap rows,
+// so a wave reads whole contiguous channel runs of the feature map
+// (coalesced), and every lane writes one 16-byte f32 vector per chunk, so
+// each store instruction covers a contiguous run of the output row.
+//
+// Each lane group takes P points per pass and issues all 4 * P * CPL tap
+// loads before it consumes any, so a wave keeps that many loads in flight
+// instead of waiting on one tap at a time.  The taps are read through a
+// buffer resource that spans the feature map: a tap outside the map gets an
+// offset past the end, which the hardware answers with zeros, and its weight
+// is set to zero, so it adds +0 to the sum, which leaves the sum bitwise as
+// it is when the tap is skipped (the sum starts at +0 and a round-to-nearest
+// sum is -0 only when both terms are).  The output is written once and not
+// read again here: non-temporal stores.  (Measured on MI355X at C = 32..512,
+// 16 frames: 8-byte f16 chunks with non-temporal stores beat 16-byte chunks,
+// whose two stores per lane each cover every other 16 bytes of a row, by up
+// to 2x; P = 2 beats P = 1 and 4.)
+constexpr uint32_t kTapOutside = 0x80000000u;  // past any feature map this kernel accepts
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// V elements of TF at byte offset off of the buffer (zeros past its end)
+template <typename TF, int V> struct tap_chunk;
+template <> struct tap_chunk<float, 4> {
+    typedef floatx4 type;
+    static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+};
+template <> struct tap_chunk<half_t, 4> {
+    typedef half4 type;
+    static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    }
+};
+template <typename TF, int V, int G, int CPL, int P>
+__global__ __launch_bounds__(256) void gather_cl_vec(const TF *__restrict__ feat, uint32_t feat_bytes,
                                                      const float *__restrict__ grid,
                                                      float *__restrict__ dst, int C, int W, int H,
                                                      int64_t N, int planar) {
 #pragma clang fp contract(off)
-    constexpr int VEC = vec16<TF>::n;
-    typedef typename vec16<TF>::type vt;
-    constexpr int PPW = 64 / G;  // points per wave
+    typedef tap_chunk<TF, V> ld;
+    typedef typename ld::type vt;
+    constexpr int CB = V * (int) sizeof(TF);  // bytes per chunk
+    constexpr int PPW = 64 / G;               // points per wave and pass
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *) feat, (short) 0, (int) feat_bytes, 0x00020000);
     const int lane = threadIdx.x & 63;
     const int gl = lane % G, grp = lane / G;
+    const uint32_t row_bytes = (uint32_t) C * sizeof(TF);
     const int64_t wave = (int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int64_t nwaves = (int64_t) gridDim.x * (blockDim.x >> 6);
-    for (int64_t n = wave * PPW + grp; n < N; n += nwaves * PPW) {
-        const float gx = planar ? grid[n] : grid[2 * n];
-        const float gy = planar ? grid[N + n] : grid[2 * n + 1];
-        const taps4 t = gather_geometry(gx, gy, W, H);
-        float acc[CPL][VEC];
+    for (int64_t n0 = wave * PPW * P + grp; n0 < N; n0 += nwaves * PPW * P) {
+        uint32_t off[P][4];
+        float w[P][4];
 #pragma unroll
-        for (int ch = 0; ch < CPL; ch++)
+        for (int p = 0; p < P; p++) {
+            const int64_t n = n0 + p * PPW < N ? n0 + p * PPW : N - 1;
+            const float gx = planar ? grid[n] : grid[2 * n];
+            const float gy = planar ? grid[N + n] : grid[2 * n + 1];
+            const taps4 t = gather_geometry(gx, gy, W, H);
 #pragma unroll
-            for (int e = 0; e < VEC; e++) acc[ch][e] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
-            if (cx < 0 || cx >= W || cy < 0 || cy >= H) continue;
-            const float w = tap_weight(t, k);
-            const TF *f = feat + (int64_t) (cy * W + cx) * C;
-#pragma unroll
-            for (int ch = 0; ch < CPL; ch++) {
-                const vt v = *(const vt *) (f + (ch * G + gl) * VEC);
-#pragma unroll
-                for (int e = 0; e < VEC; e++) acc[ch][e] += w * to_f32(v[e]);
+            for (int k = 0; k < 4; k++) {
+                const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
+                const bool in = cx >= 0 && cx < W && cy >= 0 && cy < H;
+                off[p][k] = in ? (uint32_t) (cy * W + cx) * row_bytes + gl * CB : kTapOutside;
+                w[p][k] = in ? tap_weight(t, k) : 0.0f;
             }
         }
-        float *d = dst + n * C;
+        vt v[P][4][CPL];
 #pragma unroll
-        for (int ch = 0; ch < CPL; ch++) {
-            float *dd = d + (ch * G + gl) * VEC;
+        for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int e = 0; e < VEC; e += 4)
-                *(floatx4 *) (dd + e) = floatx4{acc[ch][e], acc[ch][e + 1], acc[ch][e + 2], acc[ch][e + 3]};
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+                for (int ch = 0; ch < CPL; ch++) v[p][k][ch] = ld::load(rs, off[p][k] + ch * G * CB);
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const int64_t n = n0 + p * PPW;
+            if (n >= N) break;
+            float *d = dst + n * C;
+#pragma unroll
+            for (int ch = 0; ch < CPL; ch++) {
+                float acc[V];
+#pragma unroll
+                for (int e = 0; e < V; e++) acc[e] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+#pragma unroll
+                    for (int e = 0; e < V; e++) acc[e] += w[p][k] * to_f32(v[p][k][ch][e]);
+                float *dd = d + (ch * G + gl) * V;
+#pragma unroll
+                for (int e = 0; e < V; e += 4) {
+                    __builtin_nontemporal_store(floatx4{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]},
+                                                (floatx4 *) (dd + e));
+                }
+            }
         }
     }
 }
@@ -180,29 +232,30 @@ static int grid_for(int64_t work, int per_block) {
 template <typename TF>
 static hipError_t launch_gather_typed(const TF *feat, const float *grid, float *dst, int C, int W,
                                       int H, int64_t N, int planar, int sp, hipStream_t st) {
-    constexpr int VEC = vec16<TF>::n;
+    constexpr int VEC = 4;
     const bool aligned = (((uintptr_t) feat | (uintptr_t) dst) & 15) == 0;
-    if (!sp && C % VEC == 0 && aligned) {
+    const int64_t feat_bytes = (int64_t) W * H * C * (int64_t) sizeof(TF);
+    if (!sp && C % VEC == 0 && aligned && feat_bytes < (int64_t) kTapOutside) {
         const int lpp = C / VEC;
         int G = 0, CPL = 0;
         if (lpp <= 64 && (lpp & (lpp - 1)) == 0) {
             G = lpp;
             CPL = 1;
-        } else if (lpp % 64 == 0 && (lpp / 64 == 2 || lpp / 64 == 4)) {
+        } else if (lpp % 64 == 0 && (lpp / 64 == 2 || lpp / 64 == 4 || lpp / 64 == 8)) {
             G = 64;
             CPL = lpp / 64;
         }
         if (G) {
-            const int ppb = 4 * (64 / G);  // points per 256-thread block
-            const int nb = grid_for(N, ppb);
-#define TPMD_G(g, cpl)                                                                        \
-    if (G == g && CPL == cpl) {                                                               \
-        hipLaunchKernelGGL((gather_cl_vec<TF, g, cpl>), dim3(nb), dim3(256), 0, st, feat, grid, \
-                           dst, C, W, H, N, planar);                                          \
-        return hipGetLastError();                                                             \
+            const int P = CPL >= 4 ? 1 : 2;
+            const int nb = grid_for(N, 4 * (64 / G) * P);  // 4 waves per 256-thread block
+#define TPMD_G(g, cpl, p)                                                                          \
+    if (G == g && CPL == cpl) {                                                                    \
+        hipLaunchKernelGGL((gather_cl_vec<TF, VEC, g, cpl, p>), dim3(nb), dim3(256), 0, st, feat,  \
+                           (uint32_t) feat_bytes, grid, dst, C, W, H, N, planar);                 \
+        return hipGetLastError();                                                                  \
     }
-            TPMD_G(1, 1) TPMD_G(2, 1) TPMD_G(4, 1) TPMD_G(8, 1) TPMD_G(16, 1) TPMD_G(32, 1)
-            TPMD_G(64, 1) TPMD_G(64, 2) TPMD_G(64, 4)
+            TPMD_G(1, 1, 2) TPMD_G(2, 1, 2) TPMD_G(4, 1, 2) TPMD_G(8, 1, 2) TPMD_G(16, 1, 2)
+            TPMD_G(32, 1, 2) TPMD_G(64, 1, 2) TPMD_G(64, 2, 2) TPMD_G(64, 4, 1) TPMD_G(64, 8, 1)
 #undef TPMD_G
         }
     }
