@@ -29,7 +29,8 @@ namespace tpmd {
 // read again here: non-temporal stores.  (Measured on MI355X at C = 32..512,
 // 16 frames: 8-byte f16 chunks with non-temporal stores beat 16-byte chunks,
 // whose two stores per lane each cover every other 16 bytes of a row, by up
-// to 2x; P = 2 beats P = 1 and 4.)
+// to 2x; a grid of 4096 blocks, 16 per CU, looping over the points, beats
+// one pass per wave by up to 10 %, and P = 1 is on par with P = 2 and 4.)
 constexpr uint32_t kTapOutside = 0x80000000u;  // past any feature map this kernel accepts
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -76,9 +77,9 @@ __global__ __launch_bounds__(256) void gather_cl_vec(const TF *__restrict__ feat
             const taps4 t = gather_geometry(gx, gy, W, H);
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
-                const bool in = cx >= 0 && cx < W && cy >= 0 && cy < H;
-                off[p][k] = in ? (uint32_t) (cy * W + cx) * row_bytes + gl * CB : kTapOutside;
+                const bool in = tap_inside(t, k, W, H);
+                off[p][k] = in ? (uint32_t) ((t.y0 + (k >> 1)) * W + t.x0 + (k & 1)) * row_bytes + gl * CB
+                               : kTapOutside;
                 w[p][k] = in ? tap_weight(t, k) : 0.0f;
             }
         }
@@ -133,8 +134,8 @@ __global__ __launch_bounds__(256) void gather_elem(const TF *__restrict__ feat,
         float acc = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
+            if (!tap_inside(t, k, W, H)) continue;
             const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
-            if (cx < 0 || cx >= W || cy < 0 || cy >= H) continue;
             acc += tap_weight(t, k) * to_f32(feat[(int64_t) (cy * W + cx) * C + c]);
         }
         dst[i] = acc;
@@ -246,16 +247,17 @@ static hipError_t launch_gather_typed(const TF *feat, const float *grid, float *
             CPL = lpp / 64;
         }
         if (G) {
-            const int P = CPL >= 4 ? 1 : 2;
-            const int nb = grid_for(N, 4 * (64 / G) * P);  // 4 waves per 256-thread block
+            constexpr int P = 1;
+            int nb = grid_for(N, 4 * (64 / G) * P);  // 4 waves per 256-thread block
+            if (nb > 4096) nb = 4096;
 #define TPMD_G(g, cpl, p)                                                                          \
     if (G == g && CPL == cpl) {                                                                    \
         hipLaunchKernelGGL((gather_cl_vec<TF, VEC, g, cpl, p>), dim3(nb), dim3(256), 0, st, feat,  \
                            (uint32_t) feat_bytes, grid, dst, C, W, H, N, planar);                 \
         return hipGetLastError();                                                                  \
     }
-            TPMD_G(1, 1, 2) TPMD_G(2, 1, 2) TPMD_G(4, 1, 2) TPMD_G(8, 1, 2) TPMD_G(16, 1, 2)
-            TPMD_G(32, 1, 2) TPMD_G(64, 1, 2) TPMD_G(64, 2, 2) TPMD_G(64, 4, 1) TPMD_G(64, 8, 1)
+            TPMD_G(1, 1, P) TPMD_G(2, 1, P) TPMD_G(4, 1, P) TPMD_G(8, 1, P) TPMD_G(16, 1, P)
+            TPMD_G(32, 1, P) TPMD_G(64, 1, P) TPMD_G(64, 2, P) TPMD_G(64, 4, P) TPMD_G(64, 8, P)
 #undef TPMD_G
         }
     }

@@ -142,6 +142,14 @@ __device__ __forceinline__ taps4 gather_geometry(float gx, float gy, int W, int 
     return t;
 }
 
+// tap k (cx = x0 + (k&1), cy = y0 + (k>>1)) lies inside the W x H map.
+// Written without forming x0 + 1: an infinite coordinate converts to
+// INT_MAX / INT_MIN, and x0 + 1 would wrap into the map.
+__device__ __forceinline__ bool tap_inside(const taps4 &t, int k, int W, int H) {
+    const int dx = k & 1, dy = k >> 1;
+    return t.x0 >= -dx && t.x0 < W - dx && t.y0 >= -dy && t.y0 < H - dy;
+}
+
 // weight of tap k (cx = x0 + (k&1), cy = y0 + (k>>1))
 __device__ __forceinline__ float tap_weight(const taps4 &t, int k) {
 #pragma clang fp contract(off)

@@ -114,9 +114,10 @@ __device__ __forceinline__ void tail_pixel(const TailArgs &a, int64_t pp, bool v
     bool in[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {  // issue the four tap loads together
-        const int cx = t.x0 + (k & 1), cy = t.y0 + (k >> 1);
-        in[k] = cx >= 0 && cx < r && cy >= 0 && cy < r;
-        if (in[k]) load8<TF>::run((const TF *) a.feat + (int64_t) (cy * r + cx) * C + c0, fv[k]);
+        in[k] = tap_inside(t, k, r, r);
+        if (in[k])
+            load8<TF>::run((const TF *) a.feat + (int64_t) ((t.y0 + (k >> 1)) * r + t.x0 + (k & 1)) * C + c0,
+                           fv[k]);
     }
     float smp[8];
 #pragma unroll
@@ -374,8 +375,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
             // pixel; a tap outside the map reads the zero pad after it
             const char *gb = (const char *) a.featg;
             const unsigned gpad = (unsigned) RR * 16u;
-            const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) (t.x0 + 1) < (unsigned) r};
-            const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) (t.y0 + 1) < (unsigned) r};
+            const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) t.x0 + 1u < (unsigned) r};
+            const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) t.y0 + 1u < (unsigned) r};
             const unsigned base = (unsigned) (t.y0 * r + t.x0) * 16u;
             floatx4 gv[4];
 #pragma unroll
@@ -440,8 +441,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
             t[b].wx = q0[2];
             t[b].wy = q0[3];
             m[b] = prm[lp * L::PRM + 4];
-            const bool inx[2] = {(unsigned) t[b].x0 < (unsigned) r, (unsigned) (t[b].x0 + 1) < (unsigned) r};
-            const bool iny[2] = {(unsigned) t[b].y0 < (unsigned) r, (unsigned) (t[b].y0 + 1) < (unsigned) r};
+            const bool inx[2] = {(unsigned) t[b].x0 < (unsigned) r, (unsigned) t[b].x0 + 1u < (unsigned) r};
+            const bool iny[2] = {(unsigned) t[b].y0 < (unsigned) r, (unsigned) t[b].y0 + 1u < (unsigned) r};
             const unsigned base = ((unsigned) (t[b].y0 * r + t[b].x0) * C + c0) * (unsigned) sizeof(TF);
 #pragma unroll
             for (int k = 0; k < 4; k++) {

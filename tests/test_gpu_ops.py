@@ -23,6 +23,10 @@ def _dev(torch, a):
     (3, 9, 7, 777, -1.3, 1.3, False, False, False),         # odd C -> element kernel
     (16, 9, 7, 777, -1.3, 1.3, False, False, True),         # SP output
     (1024, 8, 8, 300, -1.2, 1.2, False, False, False),      # 4 chunks per lane
+    (2048, 8, 8, 300, -1.2, 1.2, True, False, False),       # 8 chunks per lane
+    (2048, 6, 5, 123, -1.2, 1.2, False, True, False),
+    (4, 33, 17, 5000, -1.1, 1.1, False, False, False),      # one lane per point
+    (8, 17, 33, 5000, -1.1, 1.1, True, False, False),
 ])
 def test_gather_bit_exact(om, torch_cuda, C, W, H, N, lo, hi, f16, planar, sp):
     torch = torch_cuda
@@ -36,6 +40,22 @@ def test_gather_bit_exact(om, torch_cuda, C, W, H, N, lo, hi, f16, planar, sp):
     fd = _dev(torch, feat.astype(np.float16) if f16 else feat)
     got = tpmd.gather(fd, W, H, _dev(torch, gin), planar=planar, sp=sp).cpu().numpy()
     assert got.shape == want.shape
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gather_infinite_coordinates(om, torch_cuda):
+    """grid entries of +-inf select taps outside the map (zeros), as in the
+    reference's per-tap bounds check"""
+    torch = torch_cuda
+    C, W, H, N = 64, 16, 16, 1000
+    g = np.random.default_rng(5)
+    feat = g.standard_normal((W * H, C)).astype(np.float32)
+    grid = synth.grid(N, -1.1, 1.1, seed=77, jitter=1.0, res=W)
+    grid[::7, 0] = np.inf
+    grid[3::11, 1] = -np.inf
+    want = om.bilinear_gather(feat, grid, W, H)
+    got = tpmd.gather(_dev(torch, feat), W, H, _dev(torch, grid)).cpu().numpy()
+    assert np.all(want[::7] == 0) and np.all(got[::7] == 0)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
