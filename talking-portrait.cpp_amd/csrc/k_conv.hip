@@ -298,8 +298,10 @@ static int row_bytes(int IC, int esize) { return (IC * esize) % 128 == 0 ? 128 :
 
 int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
 
-bool modconv_uses_chunk_A(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
-    return modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W);
+int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
+    if (modconv_up64_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_FRAG;
+    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_CHUNK;
+    return A_ORDER_TAP;
 }
 
 // the dense conv of an r x r stage with OC channels can run the stage tail in
@@ -426,12 +428,14 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (fused && (c.mode != MODE_DENSE || c.H != c.W || c.tail->C != c.OC || c.tail->r != c.H ||
                   (int64_t) c.tail->nframes * c.tail->r * c.tail->r != p.N))
         return hipErrorInvalidValue;
-    if (!fused && modconv_up64_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W))
-        return launch_modconv_up64(p, st);
-    // (the decoder supplies A_chunk for every conv whose decode shape this
-    // accepts; a test entry at another shape may run the tap-major kernels)
-    if (!fused && c.A_chunk && modconv_hring_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
-        p.A = c.A_chunk;
+    // (the decoder supplies A_perm for every conv whose decode shape these
+    // accept; a test entry without it runs the tap-major kernels)
+    if (!fused && modconv_up64_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
+        if (c.A_perm) p.A = c.A_perm;
+        return launch_modconv_up64(p, c.A_perm != nullptr, st);
+    }
+    if (!fused && c.A_perm && modconv_hring_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
+        p.A = c.A_perm;
         return launch_modconv_hring(p, c.mode, st);
     }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))

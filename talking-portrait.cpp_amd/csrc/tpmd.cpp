@@ -40,7 +40,7 @@ struct ConvW {
     int ic = 0, oc = 0;
     bool up = false;
     void *A = nullptr;         // act [M][9*IC], M = oc or 4*oc
-    void *A_chunk = nullptr;   // act [M][IC/32][9][32]: A in channel-chunk-major k order, or null
+    void *A_perm = nullptr;    // act: A in the order modconv_a_order names for the decode shape, or null
     float *bias = nullptr;     // [oc] activate.bias (x sqrt2)
     int64_t saug_off = 0;      // into saug_all, [oc][ic+1]
     int seg = 0;               // style segment
@@ -356,6 +356,22 @@ std::vector<float> chunk_major(const std::vector<float> &A, int M, int IC) {
     return out;
 }
 
+// A [M][9*IC] (k = tap*IC + ic) -> MFMA fragment order [9][IC/16][M/32][64][8]:
+// fragment (tap, ks) of row block w, lane l = row 32w + l%32, k = tap*IC + ks*16 + (l/32)*8 + e
+std::vector<float> fragment_order(const std::vector<float> &A, int M, int IC) {
+    const size_t K = (size_t) 9 * IC;
+    const int KS = IC / 16, MB = M / 32;
+    std::vector<float> out(A.size());
+    for (int tap = 0; tap < 9; tap++)
+        for (int ks = 0; ks < KS; ks++)
+            for (int w = 0; w < MB; w++)
+                for (int l = 0; l < 64; l++)
+                    for (int e = 0; e < 8; e++)
+                        out[((((size_t) tap * KS + ks) * MB + w) * 64 + l) * 8 + e] =
+                            A[(size_t) (w * 32 + l % 32) * K + (size_t) tap * IC + ks * 16 + (l / 32) * 8 + e];
+    return out;
+}
+
 bool check_ctx(tpmd_ctx *c) {
     if (!c) return false;
     c->err.clear();
@@ -545,9 +561,11 @@ int tpmd_prepare(tpmd_ctx *c) {
         cv.A = c->upload_act(A);
         // input map of the conv: 4 x 4 for conv1, r/2 for stage j's up-conv, r for its dense conv
         const int hin = L == 0 ? 4 : (cv.up ? 4 << j : 8 << j);
-        if (modconv_uses_chunk_A(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin)) {
-            cv.A_chunk = c->upload_act(chunk_major(A, cv.up ? 4 * cv.oc : cv.oc, cv.ic));
-            if (!cv.A_chunk) return -1;
+        const int order = modconv_a_order(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin);
+        if (order != A_ORDER_TAP) {
+            const int M = cv.up ? 4 * cv.oc : cv.oc;
+            cv.A_perm = c->upload_act(order == A_ORDER_CHUNK ? chunk_major(A, M, cv.ic) : fragment_order(A, M, cv.ic));
+            if (!cv.A_perm) return -1;
         }
         cv.bias = c->upload(ab->data);
         if (!cv.A || !cv.bias) return -1;
@@ -777,7 +795,7 @@ static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void
     a.f16 = c->f16;
     a.out_f16 = out_f16;
     a.A = cv.A;
-    a.A_chunk = cv.A_chunk;
+    a.A_perm = cv.A_perm;
     a.X = X;
     a.Y = Y;
     a.inv_den = c->L->den_all + cv.d_off;
@@ -1058,7 +1076,7 @@ int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, con
     ca.mode = cv.up ? 1 : 0;
     ca.f16 = c->f16;
     ca.A = cv.A;
-    ca.A_chunk = cv.A_chunk;
+    ca.A_perm = cv.A_perm;
     ca.X = xs;
     ca.Y = y;
     ca.inv_den = den;
@@ -1178,7 +1196,7 @@ int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float
     ca.mode = 0;
     ca.f16 = c->f16;
     ca.A = cv.A;
-    ca.A_chunk = cv.A_chunk;
+    ca.A_perm = cv.A_perm;
     ca.X = xs;
     ca.inv_den = den;
     ca.bias = cv.bias;

@@ -126,7 +126,8 @@ hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st);
 // k_conv_up.hip: f16 composed sub-pixel up-conv 64 -> 32 channels with f16
 // output, on 4 x 32 halo tiles (H % 4 == 0, W % 32 == 0)
 bool modconv_up64_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
-hipError_t launch_modconv_up64(const ConvParams &p, hipStream_t st);
+// frag: p.A in A_ORDER_FRAG order (else tap-major)
+hipError_t launch_modconv_up64(const ConvParams &p, bool frag, hipStream_t st);
 // k_conv_fused.hip: f16 dense conv + fused stage tail for IC = OC = 32 on
 // halo tiles of 8 x 32 pixels (r % 32 == 0)
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r);

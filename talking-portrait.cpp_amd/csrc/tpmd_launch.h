@@ -77,7 +77,7 @@ struct ConvArgs {
     bool f16 = false;           // operands f16 (else f32)
     bool out_f16 = false;       // stored activation f16 (f16 mode only)
     const void *A = nullptr;    // [M][9*IC], M = OC or 4*OC
-    const void *A_chunk = nullptr;  // the same in [M][IC/32][9][32] order, or null (modconv_uses_chunk_A)
+    const void *A_perm = nullptr;   // the same in the order modconv_a_order names, or null
     const void *X = nullptr;    // CL input [frame][H][W][IC], frame stride x_bstride
     void *Y = nullptr;          // CL output [frame][H'][W'][OC]
     const float *inv_den = nullptr;    // [frame][OC]
@@ -94,9 +94,16 @@ struct ConvArgs {
 };
 
 int modconv_k_align(bool f16);
-// whether the conv reads A in chunk-major order (ConvArgs::A_chunk); a
-// function of the per-frame shape only
-bool modconv_uses_chunk_A(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
+// the order in which the kernel chosen for a conv shape reads A best
+// (ConvArgs::A_perm holds that copy; a function of the per-frame shape only):
+//   A_ORDER_TAP    [M][9][IC], A itself (no copy);
+//   A_ORDER_CHUNK  [M][IC/32][9][32], channel-chunk-major k (the halo ring);
+//   A_ORDER_FRAG   [9][IC/16][M/32][64][8], MFMA fragment order: fragment
+//                  (tap, ks) of row block w at lane l holds row 32w + l%32,
+//                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the 64 -> 32 up-conv),
+//                  so a wave reads each fragment as one contiguous 1 KB.
+enum { A_ORDER_TAP = 0, A_ORDER_CHUNK = 1, A_ORDER_FRAG = 2 };
+int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
 bool modconv_fusable(int OC, int r, bool f16);
 // split-K factor of a conv (depends on the per-frame shape only)
