@@ -300,6 +300,11 @@ int modconv_k_align(bool f16) { return f16 ? 32 : 16; }
 
 int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
     if (modconv_up64_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_FRAG;
+    // the dense convs whose fused stage-tail kernels DMA A fragments (the
+    // tap-major kernels that run them unfused read A, not A_perm)
+    if (mode == MODE_DENSE && H == W && modconv_fusable(OC, H, f16) &&
+        (modconv_fused32_ok(f16, IC, OC, H) || modconv_fused64_ok(f16, IC, OC, H)))
+        return A_ORDER_FRAG;
     if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_CHUNK;
     return A_ORDER_TAP;
 }
@@ -440,10 +445,14 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
-    if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H))
-        return launch_modconv_fused32(p, *c.tail, c.trunk_f16, st);
-    if (fused && modconv_fused64_ok(c.f16, c.IC, c.OC, c.H))
-        return launch_modconv_fused64(p, *c.tail, c.trunk_f16, st);
+    if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H)) {
+        if (c.A_perm) p.A = c.A_perm;
+        return launch_modconv_fused32(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
+    }
+    if (fused && modconv_fused64_ok(c.f16, c.IC, c.OC, c.H)) {
+        if (c.A_perm) p.A = c.A_perm;
+        return launch_modconv_fused64(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
+    }
     if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H))
         return launch_modconv_tail_async(p, *c.tail, c.trunk_f16, st);
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);

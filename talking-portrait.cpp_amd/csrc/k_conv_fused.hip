@@ -8,7 +8,9 @@
 //     registers to LDS with a 16-byte pad per pixel (conflict-free 32-pixel
 //     fragment reads); the 32 x 288 weight matrix goes global -> LDS by the
 //     DMA path in MFMA fragment order (18 fragments of 1 KB, each read back
-//     by one ds_read_b128 per lane), so it holds no registers;
+//     by one ds_read_b128 per lane), so it holds no registers.  FRAG: A is
+//     stored in that order (A_ORDER_FRAG), so each fragment's DMA reads
+//     1 KB of contiguous memory instead of 32 bytes of 32 rows;
 //   * wave w computes rows w*TH/4 .. of the block: for each tap (dy, dx) and
 //     16-channel step, the B fragment is the halo row shifted by (dy, dx);
 //   * the activated tile goes to LDS over the halo and the two-phase stage
@@ -40,7 +42,7 @@ struct fused32_cfg {
     static_assert(TH % 4 == 0, "rows per wave");
 };
 
-template <typename TF, typename TT, int TH>
+template <typename TF, typename TT, int TH, bool FRAG>
 __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
                                                           int tiles_frame) {
     typedef half_t TA;
@@ -83,9 +85,9 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
     const int lrow = lane & 31, khalf = lane >> 5;
     {
         // fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
-        const TA *arow = (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
+        const TA *arow = FRAG ? (const TA *) p.A + lane * 8 : (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
         for (int f = wid; f < NAF; f += NT / 64)
-            __builtin_amdgcn_global_load_lds((const void *) (arow + f * 16),
+            __builtin_amdgcn_global_load_lds((const void *) (arow + f * (FRAG ? 512 : 16)),
                                              (__attribute__((address_space(3))) void *) (smem + F::AOFF + f * 1024),
                                              16, 0, 0);
     }
@@ -144,7 +146,8 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
 // matrix is too large to keep, so it streams through a 2-stage LDS ring by
 // the DMA path, one tap (8 fragments of 1 KB) at a time, shared by the four
 // waves; wave w computes weight rows 32*(w&1) .. +31 for block rows
-// 2*(w>>1) .. +1.
+// 2*(w>>1) .. +1.  FRAG: A in fragment order (A_ORDER_FRAG), contiguous
+// 1 KB per fragment DMA.
 struct fused64_cfg {
     static constexpr int C = 64, NT = 256, TH = 4, TW = 32, BN = TH * TW;
     static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
@@ -169,7 +172,7 @@ struct fused64_cfg {
 // s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt not waited on
 constexpr int fused_waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
 
-template <typename TF, typename TT>
+template <typename TF, typename TT, bool FRAG>
 __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
                                                           int tiles_frame) {
     typedef half_t TA;
@@ -201,7 +204,8 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
         char *stage = smem + F::AOFF + (t & 1) * F::ASTG;
         static_for<APW>([&](auto j) {
             const int f = wid * APW + j;
-            const TA *src = Ab + (int64_t) ((f & 1) * 32 + lrow) * K + t * C + (f >> 1) * 16 + khalf * 8;
+            const TA *src = FRAG ? Ab + (t * FPT + f) * 512 + lane * 8
+                                 : Ab + (int64_t) ((f & 1) * 32 + lrow) * K + t * C + (f >> 1) * 16 + khalf * 8;
             __builtin_amdgcn_global_load_lds((const void *) src,
                                              (__attribute__((address_space(3))) void *) (stage + f * 1024), 16, 0, 0);
         });
@@ -284,35 +288,45 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
 
 bool modconv_fused64_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 64 && OC == 64 && r % 32 == 0; }
 
-hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
+hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
+                                  hipStream_t st) {
     if (p.IC != 64 || p.OC != 64 || p.M != 64 || p.W % 32 != 0 || p.H % fused64_cfg::TH != 0)
         return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / fused64_cfg::TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
-    if (trunk_f16)
-        hipLaunchKernelGGL((conv64_tail_kernel<half_t, half_t>), grid, dim3(256), 0, st, p, ta, tiles_x,
-                           tiles_frame);
-    else
-        hipLaunchKernelGGL((conv64_tail_kernel<half_t, float>), grid, dim3(256), 0, st, p, ta, tiles_x,
-                           tiles_frame);
+#define TPMD_L(TT, FR) \
+    hipLaunchKernelGGL((conv64_tail_kernel<half_t, TT, FR>), grid, dim3(256), 0, st, p, ta, tiles_x, tiles_frame)
+    if (trunk_f16) {
+        if (frag) TPMD_L(half_t, true);
+        else TPMD_L(half_t, false);
+    } else {
+        if (frag) TPMD_L(float, true);
+        else TPMD_L(float, false);
+    }
+#undef TPMD_L
     return hipGetLastError();
 }
 
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 32 && OC == 32 && r % 32 == 0; }
 
-hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
+hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
+                                  hipStream_t st) {
     constexpr int TH = 8;
     if (p.IC != 32 || p.OC != 32 || p.M != 32 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
-    if (trunk_f16)
-        hipLaunchKernelGGL((conv32_tail_kernel<half_t, half_t, TH>), grid, dim3(256), 0, st, p, ta, tiles_x,
-                           tiles_frame);
-    else
-        hipLaunchKernelGGL((conv32_tail_kernel<half_t, float, TH>), grid, dim3(256), 0, st, p, ta, tiles_x,
-                           tiles_frame);
+#define TPMD_L(TT, FR) \
+    hipLaunchKernelGGL((conv32_tail_kernel<half_t, TT, TH, FR>), grid, dim3(256), 0, st, p, ta, tiles_x, tiles_frame)
+    if (trunk_f16) {
+        if (frag) TPMD_L(half_t, true);
+        else TPMD_L(half_t, false);
+    } else {
+        if (frag) TPMD_L(float, true);
+        else TPMD_L(float, false);
+    }
+#undef TPMD_L
     return hipGetLastError();
 }
 

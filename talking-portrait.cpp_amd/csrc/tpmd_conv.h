@@ -131,10 +131,13 @@ hipError_t launch_modconv_up64(const ConvParams &p, bool frag, hipStream_t st);
 // k_conv_fused.hip: f16 dense conv + fused stage tail for IC = OC = 32 on
 // halo tiles of 8 x 32 pixels (r % 32 == 0)
 bool modconv_fused32_ok(bool f16, int IC, int OC, int r);
-hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
+// frag: p.A in A_ORDER_FRAG order (else tap-major)
+hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
+                                  hipStream_t st);
 // ... and for IC = OC = 64 on 4 x 32 halo tiles, A streamed through LDS per tap
 bool modconv_fused64_ok(bool f16, int IC, int OC, int r);
-hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
+hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
+                                  hipStream_t st);
 hipError_t launch_modconv_tail_async(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
 
 }  // namespace tpmd

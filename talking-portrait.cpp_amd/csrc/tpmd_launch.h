@@ -100,8 +100,9 @@ int modconv_k_align(bool f16);
 //   A_ORDER_CHUNK  [M][IC/32][9][32], channel-chunk-major k (the halo ring);
 //   A_ORDER_FRAG   [9][IC/16][M/32][64][8], MFMA fragment order: fragment
 //                  (tap, ks) of row block w at lane l holds row 32w + l%32,
-//                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the 64 -> 32 up-conv),
-//                  so a wave reads each fragment as one contiguous 1 KB.
+//                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the 64 -> 32 up-conv
+//                  and the fused 32- and 64-channel dense convs), so a wave
+//                  reads each fragment as one contiguous 1 KB.
 enum { A_ORDER_TAP = 0, A_ORDER_CHUNK = 1, A_ORDER_FRAG = 2 };
 int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
