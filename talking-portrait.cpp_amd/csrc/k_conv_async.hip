@@ -472,15 +472,17 @@ struct hring_cfg {
     static constexpr int LDS = CONV > OUT ? CONV : OUT;
 };
 
-template <int MODE, int S>
-__global__ __launch_bounds__(512) void modconv3x3_hring_kernel(ConvParams p, int tiles_x, int tiles_frame) {
+template <int MODE, int S, int NW>
+__global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p, int tiles_x, int tiles_frame) {
     typedef half_t TA;
     typedef hring_cfg<S> C;
-    constexpr int BM = C::BM, BN = C::BN, WN = 4, NT = 512, NW = 8;
+    // NW = 8: 2 x 4 waves of 128 x 64; NW = 4: 2 x 2 waves of 128 x 128
+    // (accumulators in AGPRs, one wave per SIMD, 2/3 of the LDS fragment reads)
+    constexpr int BM = C::BM, BN = C::BN, WN = NW / 2, NT = NW * 64;
     constexpr int RB = C::RB, BK = RB / 2;
     constexpr int LPA = BM / 16 / NW;                  // A DMA instructions per wave per k tile
     constexpr int LPH = HR_HBUF / 1024 / NW;           // halo DMA instructions per wave per chunk
-    constexpr int WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
+    constexpr int WTM = 128, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
     static_assert(S >= 3 && S <= 8, "ring stages");
     __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
@@ -549,8 +551,8 @@ __global__ __launch_bounds__(512) void modconv3x3_hring_kernel(ConvParams p, int
 
     const int lrow = lane & 31;
     const int khalf = lane >> 5;
-    // this lane's halo pixel for tap (0, 0) of fragment b: block row 2*wn + b, column lrow
-    const int hbase = C::HOFF + ((2 * wn) * HR_HWD + lrow) * HR_PXB + khalf * 16;
+    // this lane's halo pixel for tap (0, 0) of fragment b: block row TN*wn + b, column lrow
+    const int hbase = C::HOFF + ((TN * wn) * HR_HWD + lrow) * HR_PXB + khalf * 16;
     auto read_frags = [&](int t, int ks, u32x4 (&af)[TM], u32x4 (&bf)[TN]) {
         const char *st = smem + (t % S) * C::ASTAGE;
         const int kc = ks * 2 + khalf;
@@ -661,6 +663,9 @@ bool modconv_hring_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, i
 
 hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st) {
     constexpr int S = 6;  // 16 KB A stages: six fill the LDS with the two halo buffers (measured: 4 -> 6 saves ~3%)
+    // 8 waves: 4 waves of 128 x 128 (one per SIMD) measured 6-15 % slower on
+    // the r64-r256 up-convs, each barrier left with no other wave to cover it
+    constexpr int NW = 8;
     if (p.M % 256 != 0 || p.IC % 32 != 0 || p.H % HR_TH != 0 || p.W % HR_TW != 0) return hipErrorInvalidValue;
     const int64_t HW = (int64_t) p.H * p.W;
     if (p.N % HW != 0) return hipErrorInvalidValue;
@@ -669,11 +674,11 @@ hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st) {
     const int tiles_x = p.W / HR_TW, tiles_frame = tiles_x * (p.H / HR_TH);
     const int64_t tiles = (int64_t) p.MT * (p.N / HW) * tiles_frame;
     if (mode == MODE_DENSE)
-        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_DENSE, S>), dim3((unsigned) tiles), dim3(512), 0, st, p,
-                           tiles_x, tiles_frame);
+        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_DENSE, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0, st,
+                           p, tiles_x, tiles_frame);
     else
-        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_SUBPIX, S>), dim3((unsigned) tiles), dim3(512), 0, st, p,
-                           tiles_x, tiles_frame);
+        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_SUBPIX, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0,
+                           st, p, tiles_x, tiles_frame);
     return hipGetLastError();
 }
 
