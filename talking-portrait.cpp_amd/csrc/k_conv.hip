@@ -305,7 +305,7 @@ int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int
     if (mode == MODE_DENSE && H == W && modconv_fusable(OC, H, f16) &&
         (modconv_fused32_ok(f16, IC, OC, H) || modconv_fused64_ok(f16, IC, OC, H)))
         return A_ORDER_FRAG;
-    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_CHUNK;
+    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_RING;
     return A_ORDER_TAP;
 }
 

@@ -451,7 +451,7 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
 // im2col tile (f16 output, every tile inside one frame): a tile is 256 GEMM
 // rows x an 8 x 32 block of pixels, and the k order is channel-chunk major,
 // k tile t = c*9 + tap (32 channels c*32 .. +31 of tap `tap`; A is stored in
-// that order, [M][IC/32][9][32]).  Per chunk the 10 x 34 halo of those 32
+// that k order, laid out as the A DMA's LDS image, A_ORDER_RING).  Per chunk the 10 x 34 halo of those 32
 // channels is fetched once by the DMA path into one of two halo buffers
 // (80-byte pixels: 4 chunks of 8 channels + a pad chunk, so 32 consecutive
 // pixels read at any offset hit distinct banks), and its 9 taps read it
@@ -500,15 +500,14 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
     const int K = 9 * IC;
     const int NC = IC / BK, T = 9 * NC;
 
-    // A DMA: instruction j of a wave moves 16 rows; lane i carries chunk
-    // (i % 4) ^ swz(row) of row i / 4; k tile t is columns t*BK .. of A
-    const int lrow16 = lane >> 2, lpos = lane & 3;
+    // A DMA: instruction j of a wave moves the 16-row block g = m0/16 +
+    // wid*LPA + j; A is stored in that DMA's LDS image order (A_ORDER_RING:
+    // lane i carries chunk (i % 4) ^ swz(row) of row i / 4), so block (g, t)
+    // is 1 KB of contiguous memory at (g*T + t) KB
     const TA *asrc[LPA];
 #pragma unroll
-    for (int j = 0; j < LPA; j++) {
-        const int row = (wid * LPA + j) * 16 + lrow16;
-        asrc[j] = (const TA *) p.A + (int64_t) (m0 + row) * K + (lpos ^ swz(row)) * 8;
-    }
+    for (int j = 0; j < LPA; j++)
+        asrc[j] = (const TA *) p.A + ((int64_t) (m0 / 16 + wid * LPA + j) * T) * 512 + lane * 8;
     // halo DMA: instruction h of a wave fills the 16-byte unit u = (wid*LPH + h)*64 + lane
     // of a halo buffer: halo pixel u / 5, channel chunk u % 5 (4: the pad);
     // units past the halo, pads and pixels outside the map read zeros
@@ -529,7 +528,7 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
     auto issue_a = [&](int t) {
         char *stage = smem + (t % S) * C::ASTAGE;
         static_for<LPA>([&](auto j) {
-            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + t * BK),
+            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + t * 512),
                                              TPMD_LDS(stage + (wid * LPA + j) * 16 * RB), 16, 0, 0);
         });
     };

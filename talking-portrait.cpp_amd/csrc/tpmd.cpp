@@ -356,6 +356,25 @@ std::vector<float> chunk_major(const std::vector<float> &A, int M, int IC) {
     return out;
 }
 
+// A [M][9*IC] -> the halo ring's DMA order [M/16][T = 9*IC/32][64][8]: block
+// (g, t), lane i = row 16g + i/4, chunk (i%4) ^ swz(row) of k tile t of the
+// chunk-major A (the LDS image the ring's DMA writes, row-swizzled)
+std::vector<float> ring_order(const std::vector<float> &A, int M, int IC) {
+    const std::vector<float> ck = chunk_major(A, M, IC);
+    const size_t K = (size_t) 9 * IC;
+    const int T = 9 * IC / 32;
+    std::vector<float> out(A.size());
+    for (int g = 0; g < M / 16; g++)
+        for (int t = 0; t < T; t++)
+            for (int i = 0; i < 64; i++) {
+                const int row = g * 16 + i / 4;
+                const int chunk = (i % 4) ^ (((row >> 2) ^ (row >> 3)) & 3);
+                for (int e = 0; e < 8; e++)
+                    out[(((size_t) g * T + t) * 64 + i) * 8 + e] = ck[row * K + (size_t) t * 32 + chunk * 8 + e];
+            }
+    return out;
+}
+
 // A [M][9*IC] (k = tap*IC + ic) -> MFMA fragment order [9][IC/16][M/32][64][8]:
 // fragment (tap, ks) of row block w, lane l = row 32w + l%32, k = tap*IC + ks*16 + (l/32)*8 + e
 std::vector<float> fragment_order(const std::vector<float> &A, int M, int IC) {
@@ -564,7 +583,7 @@ int tpmd_prepare(tpmd_ctx *c) {
         const int order = modconv_a_order(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin);
         if (order != A_ORDER_TAP) {
             const int M = cv.up ? 4 * cv.oc : cv.oc;
-            cv.A_perm = c->upload_act(order == A_ORDER_CHUNK ? chunk_major(A, M, cv.ic) : fragment_order(A, M, cv.ic));
+            cv.A_perm = c->upload_act(order == A_ORDER_RING ? ring_order(A, M, cv.ic) : fragment_order(A, M, cv.ic));
             if (!cv.A_perm) return -1;
         }
         cv.bias = c->upload(ab->data);
