@@ -305,6 +305,8 @@ int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int
     if (mode == MODE_DENSE && H == W && modconv_fusable(OC, H, f16) &&
         (modconv_fused32_ok(f16, IC, OC, H) || modconv_fused64_ok(f16, IC, OC, H)))
         return A_ORDER_FRAG;
+    if (mode == MODE_DENSE && H == W && f16 && OC == 256 && IC % 32 == 0 && modconv_fusable(OC, H, f16))
+        return A_ORDER_RING_TAP;
     if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_RING;
     return A_ORDER_TAP;
 }
@@ -453,8 +455,13 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
         if (c.A_perm) p.A = c.A_perm;
         return launch_modconv_fused64(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
     }
-    if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H))
+    if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H)) {
+        if (c.A_perm && c.OC == 256) {
+            p.A = c.A_perm;
+            p.a_img = 1;
+        }
         return launch_modconv_tail_async(p, *c.tail, c.trunk_f16, st);
+    }
     int nsplit = fused ? 1 : modconv_splits(c.mode, c.H, c.W, c.IC, c.OC, c.f16);
     if (nsplit > 1 && (!c.ws || c.ws_elems < (int64_t) nsplit * p.M * p.N)) nsplit = 1;
     const int epi = fused ? EPI_TAIL : (nsplit > 1 ? EPI_PARTIAL : EPI_STORE);

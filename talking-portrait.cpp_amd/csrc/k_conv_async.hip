@@ -341,7 +341,8 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
         src[j] = Xp;
         smask[j] = 0;
         if (row < BM) {
-            src[j] = Ap + (int64_t) row * K + chunk;
+            // (a_img: row group g's k tile t is the 1 KB block (g*T + t) of A)
+            src[j] = p.a_img ? Ap + (int64_t) (row >> 4) * T * 512 + lane * 8 : Ap + (int64_t) row * K + chunk;
             smask[j] = 0x1FFu;
         } else if (row < BM + BN) {
             const int rem = n0 - fr * HW + row - BM;
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
         static_for<SLOTS>([&](auto j) {
             const int g = j * NW + wid;
             if (g < NG) {
-                const int off = g < BM / 16 ? q_t * BK : boff;
+                const int off = g < BM / 16 ? q_t * (p.a_img ? 512 : BK) : boff;
                 const void *gp = (smask[j] >> q_tap) & 1u ? (const void *) (src[j] + off) : zero;
                 __builtin_amdgcn_global_load_lds(gp, TPMD_LDS(stage + g * 16 * RB), 16, 0, 0);
             }

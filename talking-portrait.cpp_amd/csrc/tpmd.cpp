@@ -356,14 +356,13 @@ std::vector<float> chunk_major(const std::vector<float> &A, int M, int IC) {
     return out;
 }
 
-// A [M][9*IC] -> the halo ring's DMA order [M/16][T = 9*IC/32][64][8]: block
-// (g, t), lane i = row 16g + i/4, chunk (i%4) ^ swz(row) of k tile t of the
-// chunk-major A (the LDS image the ring's DMA writes, row-swizzled)
-std::vector<float> ring_order(const std::vector<float> &A, int M, int IC) {
-    const std::vector<float> ck = chunk_major(A, M, IC);
+// A [M][K = 9*IC] in some k order -> the LDS rings' DMA order [M/16][T = K/32][64][8]:
+// block (g, t), lane i = row 16g + i/4, chunk (i%4) ^ swz(row) of k tile t
+// (the row-swizzled LDS image the DMA writes)
+std::vector<float> dma_image(const std::vector<float> &ck, int M, int IC) {
     const size_t K = (size_t) 9 * IC;
     const int T = 9 * IC / 32;
-    std::vector<float> out(A.size());
+    std::vector<float> out(ck.size());
     for (int g = 0; g < M / 16; g++)
         for (int t = 0; t < T; t++)
             for (int i = 0; i < 64; i++) {
@@ -374,6 +373,8 @@ std::vector<float> ring_order(const std::vector<float> &A, int M, int IC) {
             }
     return out;
 }
+// the halo ring's copy: channel-chunk-major k; the fused r64 ring's: tap-major k
+std::vector<float> ring_order(const std::vector<float> &A, int M, int IC) { return dma_image(chunk_major(A, M, IC), M, IC); }
 
 // A [M][9*IC] (k = tap*IC + ic) -> MFMA fragment order [9][IC/16][M/32][64][8]:
 // fragment (tap, ks) of row block w, lane l = row 32w + l%32, k = tap*IC + ks*16 + (l/32)*8 + e
@@ -583,7 +584,9 @@ int tpmd_prepare(tpmd_ctx *c) {
         const int order = modconv_a_order(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin);
         if (order != A_ORDER_TAP) {
             const int M = cv.up ? 4 * cv.oc : cv.oc;
-            cv.A_perm = c->upload_act(order == A_ORDER_RING ? ring_order(A, M, cv.ic) : fragment_order(A, M, cv.ic));
+            cv.A_perm = c->upload_act(order == A_ORDER_RING       ? ring_order(A, M, cv.ic)
+                                      : order == A_ORDER_RING_TAP ? dma_image(A, M, cv.ic)
+                                                                  : fragment_order(A, M, cv.ic));
             if (!cv.A_perm) return -1;
         }
         cv.bias = c->upload(ab->data);

@@ -67,6 +67,7 @@ struct ConvParams {
     int MT;                 // M tiles
     int T;                  // k tiles (9 * IC / BK)
     int64_t x_bstride;
+    int a_img;              // A is stored as the k-tile DMA's LDS image (A_ORDER_RING_TAP)
 };
 
 // hardware hands workgroup ids to the 8 XCDs round robin; renumber so each

@@ -107,7 +107,9 @@ int modconv_k_align(bool f16);
 //                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the 64 -> 32 up-conv
 //                  and the fused 32- and 64-channel dense convs), so a wave
 //                  reads each fragment as one contiguous 1 KB.
-enum { A_ORDER_TAP = 0, A_ORDER_RING = 1, A_ORDER_FRAG = 2 };
+//   A_ORDER_RING_TAP  the same image over tap-major k tiles (the fused
+//                  256-channel dense conv's LDS ring, r64).
+enum { A_ORDER_TAP = 0, A_ORDER_RING = 1, A_ORDER_FRAG = 2, A_ORDER_RING_TAP = 3 };
 int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
 bool modconv_fusable(int OC, int r, bool f16);
