@@ -66,9 +66,12 @@ struct tpfm_ctx {
         bool f16 = false;
         int out = 0, in = 0;
     };
-    Lin cemb, xemb, fin_mod, fin_lin;
+    Lin cemb, xemb, fin_lin;
+    // every adaLN modulation (each block's 6H rows, then the final layer's 2H)
+    // reads the same silu(c): one stacked layer, one GEMM per forward
+    Lin mods;
     struct Block {
-        Lin mod, qkv, proj, fc1, fc2;
+        Lin qkv, proj, fc1, fc2;
     };
     std::vector<Block> blocks;
     float *t0w = nullptr, *t0b = nullptr, *t2w = nullptr, *t2b = nullptr;  // t-embedder (GEMV, f32 values)
@@ -79,7 +82,7 @@ struct tpfm_ctx {
     // activations
     float *tfk = nullptr, *tf = nullptr, *te0 = nullptr, *te = nullptr;
     float *cond_f = nullptr, *clin = nullptr, *x60 = nullptr, *x1 = nullptr, *x = nullptr;
-    float *mod = nullptr, *qkv = nullptr, *fmod = nullptr, *v = nullptr;
+    float *mod = nullptr, *qkv = nullptr, *v = nullptr;  // mod: [rows][mods.out]
     float *ws = nullptr;  // split-K partials
     void *cond_a = nullptr, *sc_a = nullptr, *x60_a = nullptr, *h_a = nullptr, *o_a = nullptr, *m1_a = nullptr;
 
@@ -175,17 +178,33 @@ void make_tensor_list(tpfm_ctx *c) {
     add("decoder.linear.bias", {c->cfg.dim_w});
 }
 
-// weight [out][in] -> operand [out][in_pad] (zero columns past in), f16 when kept f16
-bool make_lin(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::string &base, int out, int in, int in_pad) {
-    const FTensor *w = c->need(base + ".weight"), *b = c->need(base + ".bias");
-    if (!w || !b) return false;
+// weights [out_j][in] of the layers `bases` (rows stacked in that order) ->
+// operand [sum out_j][in_pad] (zero columns past in), f16 when kept f16 (all
+// stacked layers must agree), biases stacked alike
+bool make_lin_stack(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::vector<std::pair<std::string, int>> &bases, int in,
+                    int in_pad) {
+    int out = 0;
+    for (const auto &bo : bases) out += bo.second;
     L.out = out;
     L.in = in_pad;
-    L.f16 = c->kept16(*w);
-    const std::vector<float> dv = c->dev_value(*w);
-    std::vector<float> a((size_t) out * in_pad, 0.0f);
-    for (int o = 0; o < out; o++)
-        for (int i = 0; i < in; i++) a[(size_t) o * in_pad + i] = dv[(size_t) o * in + i];
+    std::vector<float> a((size_t) out * in_pad, 0.0f), bias;
+    int o0 = 0;
+    for (size_t j = 0; j < bases.size(); j++) {
+        const FTensor *w = c->need(bases[j].first + ".weight"), *b = c->need(bases[j].first + ".bias");
+        if (!w || !b) return false;
+        const bool f16 = c->kept16(*w);
+        if (j == 0) L.f16 = f16;
+        else if (f16 != L.f16) {
+            c->err = "tpfm_prepare: " + bases[0].first + " and " + bases[j].first + " stored with mixed types";
+            return false;
+        }
+        const int oj = bases[j].second;
+        const std::vector<float> dv = c->dev_value(*w);
+        for (int o = 0; o < oj; o++)
+            for (int i = 0; i < in; i++) a[(size_t) (o0 + o) * in_pad + i] = dv[(size_t) o * in + i];
+        bias.insert(bias.end(), b->data.begin(), b->data.end());
+        o0 += oj;
+    }
     if (L.f16) {
         std::vector<_Float16> h(a.size());
         for (size_t i = 0; i < a.size(); i++) h[i] = (_Float16) a[i];
@@ -193,8 +212,12 @@ bool make_lin(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::string &base, int out, i
     } else {
         L.W = c->upload(a);
     }
-    L.b = c->upload(b->data);
+    L.b = c->upload(bias);
     return L.W && L.b;
+}
+
+bool make_lin(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::string &base, int out, int in, int in_pad) {
+    return make_lin_stack(c, L, {{base, out}}, in, in_pad);
 }
 
 // y[rows][L.out] (+ gate, residual, activation, operand copy) = X[rows][L.in] L.W^T + L.b
@@ -239,7 +262,7 @@ bool enqueue_forward(tpfm_ctx *c, float t) {
         !c->hip_ok(launch_enc_linear(c->t2w, c->t2b, c->te0, H, H, c->t2_16, c->te, st), "t_embed"))
         return false;
     // c = c_embed(cond) + t_emb; the adaLN layers read silu(c)
-    const bool sc16 = c->blocks.empty() ? c->fin_mod.f16 : c->blocks[0].mod.f16;
+    const bool sc16 = c->mods.f16;
     if (!linear(c, c->cemb, c->cond_a, R, c->clin, nullptr, false, 0) ||
         !c->hip_ok(launch_fmt_cond(c->clin, c->te, R, H, c->sc_a, sc16, st), "cond"))
         return false;
@@ -248,26 +271,29 @@ bool enqueue_forward(tpfm_ctx *c, float t) {
         !linear(c, c->xemb, c->x60_a, T, c->x1, nullptr, false, 0) ||
         !c->hip_ok(launch_fmt_xpos(c->x1, c->pos, T, H, c->B, c->x, st), "pos"))
         return false;
-    const int64_t ms = 6 * (int64_t) H;
-    for (const auto &Bk : c->blocks) {
-        if (!linear(c, Bk.mod, c->sc_a, R, c->mod, nullptr, false, 0)) return false;
+    // all adaLN modulations at once: block i's shift/scale/gate at columns 6H i .. of mod
+    const int64_t ms = c->mods.out;
+    if (!linear(c, c->mods, c->sc_a, R, c->mod, nullptr, false, 0)) return false;
+    for (size_t i = 0; i < c->blocks.size(); i++) {
+        const auto &Bk = c->blocks[i];
+        const float *md = c->mod + i * 6 * (size_t) H;
         // attention branch
-        if (!c->hip_ok(launch_fmt_ln_mod(c->x, c->mod, ms, 0, H, R, H, g.ln_eps, c->h_a, Bk.qkv.f16, st), "norm") ||
+        if (!c->hip_ok(launch_fmt_ln_mod(c->x, md, ms, 0, H, R, H, g.ln_eps, c->h_a, Bk.qkv.f16, st), "norm") ||
             !linear(c, Bk.qkv, c->h_a, R, c->qkv, nullptr, false, 0) ||
             !c->hip_ok(launch_fmt_attn(c->qkv, c->B, T, H, g.n_heads, g.attn_window, c->o_a, Bk.proj.f16, st),
                        "attention") ||
-            !linear(c, Bk.proj, c->o_a, R, c->x, nullptr, false, 0, c->mod + 2 * H, ms, c->x))
+            !linear(c, Bk.proj, c->o_a, R, c->x, nullptr, false, 0, md + 2 * H, ms, c->x))
             return false;
         // MLP branch
-        if (!c->hip_ok(launch_fmt_ln_mod(c->x, c->mod, ms, 3 * H, 4 * H, R, H, g.ln_eps, c->h_a, Bk.fc1.f16, st),
+        if (!c->hip_ok(launch_fmt_ln_mod(c->x, md, ms, 3 * H, 4 * H, R, H, g.ln_eps, c->h_a, Bk.fc1.f16, st),
                        "norm") ||
             !linear(c, Bk.fc1, c->h_a, R, nullptr, c->m1_a, Bk.fc2.f16, 2) ||
-            !linear(c, Bk.fc2, c->m1_a, R, c->x, nullptr, false, 0, c->mod + 5 * H, ms, c->x))
+            !linear(c, Bk.fc2, c->m1_a, R, c->x, nullptr, false, 0, md + 5 * H, ms, c->x))
             return false;
     }
     // final head
-    if (!linear(c, c->fin_mod, c->sc_a, R, c->fmod, nullptr, false, 0) ||
-        !c->hip_ok(launch_fmt_ln_mod(c->x, c->fmod, 2 * (int64_t) H, 0, H, R, H, g.ln_eps, c->h_a, c->fin_lin.f16, st),
+    const float *fmd = c->mod + c->blocks.size() * 6 * (size_t) H;
+    if (!c->hip_ok(launch_fmt_ln_mod(c->x, fmd, ms, 0, H, R, H, g.ln_eps, c->h_a, c->fin_lin.f16, st),
                    "norm") ||
         !linear(c, c->fin_lin, c->h_a, R, c->v, nullptr, false, 0))
         return false;
@@ -403,20 +429,18 @@ int tpfm_prepare(tpfm_ctx *c) {
     for (int i = 0; i < g.depth; i++) {
         auto &B = c->blocks[(size_t) i];
         const std::string b = ffmt("blocks.%d", i);
-        if (!make_lin(c, B.mod, b + ".adaLN_modulation.1", 6 * H, H, H) ||
-            !make_lin(c, B.qkv, b + ".attn.qkv", 3 * H, H, H) || !make_lin(c, B.proj, b + ".attn.proj", H, H, H) ||
+        if (!make_lin(c, B.qkv, b + ".attn.qkv", 3 * H, H, H) || !make_lin(c, B.proj, b + ".attn.proj", H, H, H) ||
             !make_lin(c, B.fc1, b + ".mlp.fc1", c->MLP, H, H) || !make_lin(c, B.fc2, b + ".mlp.fc2", H, c->MLP, c->MLP))
             return -1;
     }
-    if (!make_lin(c, c->fin_mod, "decoder.adaLN_modulation.1", 2 * H, H, H) ||
-        !make_lin(c, c->fin_lin, "decoder.linear", g.dim_w, H, H))
-        return -1;
-    // silu(c) is one operand buffer for every adaLN layer: they share a type
-    for (const auto &B : c->blocks)
-        if (B.mod.f16 != c->fin_mod.f16) {
-            c->err = "tpfm_prepare: adaLN weights stored with mixed types";
+    {
+        std::vector<std::pair<std::string, int>> mb;
+        for (int i = 0; i < g.depth; i++) mb.push_back({ffmt("blocks.%d.adaLN_modulation.1", i), 6 * H});
+        mb.push_back({"decoder.adaLN_modulation.1", 2 * H});
+        // (silu(c) is one operand buffer for every adaLN layer: they share a type)
+        if (!make_lin_stack(c, c->mods, mb, H, H) || !make_lin(c, c->fin_lin, "decoder.linear", g.dim_w, H, H))
             return -1;
-        }
+    }
     auto F = [&](size_t n) { return (float *) c->dalloc(n * 4); };
     auto A = [&](size_t n) { return c->dalloc(n * 4); };  // operand buffers sized for f32
     c->tf = F((size_t) g.t_freq_dim);
@@ -431,12 +455,11 @@ int tpfm_prepare(tpfm_ctx *c) {
     c->x60_a = A((size_t) T * g.dim_w);
     c->x1 = F((size_t) T * H);
     c->x = F((size_t) R * H);
-    c->mod = F((size_t) R * 6 * H);
+    c->mod = F((size_t) R * c->mods.out);
     c->h_a = A((size_t) R * std::max(H, g.dim_w));
     c->qkv = F((size_t) R * 3 * H);
     c->o_a = A((size_t) R * H);
     c->m1_a = A((size_t) R * c->MLP);
-    c->fmod = F((size_t) R * 2 * H);
     c->v = F((size_t) R * g.dim_w);
     {
         size_t wsn = 1;
@@ -446,10 +469,9 @@ int tpfm_prepare(tpfm_ctx *c) {
         };
         need_ws(c->cemb, R);
         need_ws(c->xemb, T);
-        need_ws(c->fin_mod, R);
+        need_ws(c->mods, R);
         need_ws(c->fin_lin, R);
         for (const auto &B : c->blocks) {
-            need_ws(B.mod, R);
             need_ws(B.qkv, R);
             need_ws(B.proj, R);
             need_ws(B.fc1, R);
@@ -458,7 +480,7 @@ int tpfm_prepare(tpfm_ctx *c) {
         c->ws = F(wsn);
     }
     if (!c->tf || !c->tfk || !c->te0 || !c->te || !c->cond_f || !c->cond_a || !c->clin || !c->sc_a || !c->x60 || !c->x60_a ||
-        !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->fmod || !c->v || !c->ws)
+        !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->v || !c->ws)
         return -1;
     c->prepared = true;
     return 0;
