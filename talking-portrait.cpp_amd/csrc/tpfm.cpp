@@ -248,8 +248,14 @@ bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float 
     return c->hip_ok(launch_enc_conv(p, L.f16, c->stream), "linear");
 }
 
-// the CFG-batched forward on device buffers: x60 (f32 [T][dim_w]) and cond_a
-// (operand rows [B*T][CDp]) are in place; v (f32 [B*T][dim_w]) is the result
+// c_embed(cond) into clin, from the condition rows in cond_a: the same for
+// every ODE step of a chunk, so it runs once per chunk
+bool enqueue_cond_embed(tpfm_ctx *c) {
+    return linear(c, c->cemb, c->cond_a, c->B * c->T, c->clin, nullptr, false, 0);
+}
+
+// the CFG-batched forward on device buffers: x60 (f32 [T][dim_w]) and clin
+// (c_embed(cond), f32 [B*T][H]) are in place; v (f32 [B*T][dim_w]) is the result
 bool enqueue_forward(tpfm_ctx *c, float t) {
     const tpfm_config &g = c->cfg;
     const int H = g.dim_h, T = c->T, R = c->B * T;
@@ -263,9 +269,7 @@ bool enqueue_forward(tpfm_ctx *c, float t) {
         return false;
     // c = c_embed(cond) + t_emb; the adaLN layers read silu(c)
     const bool sc16 = c->mods.f16;
-    if (!linear(c, c->cemb, c->cond_a, R, c->clin, nullptr, false, 0) ||
-        !c->hip_ok(launch_fmt_cond(c->clin, c->te, R, H, c->sc_a, sc16, st), "cond"))
-        return false;
+    if (!c->hip_ok(launch_fmt_cond(c->clin, c->te, R, H, c->sc_a, sc16, st), "cond")) return false;
     // x = x_embed(x60) + pos, shared by the branches
     if (!c->hip_ok(launch_fmt_convert(c->x60, T, g.dim_w, g.dim_w, c->x60_a, c->xemb.f16, st), "x60") ||
         !linear(c, c->xemb, c->x60_a, T, c->x1, nullptr, false, 0) ||
@@ -502,7 +506,7 @@ int tpfm_forward(tpfm_ctx *c, const float *x60, const float *cond, float t, floa
         !c->hip_ok(hipMemcpyAsync(c->cond_f, cond, (size_t) R * c->CD * 4, hipMemcpyHostToDevice, st), "cond") ||
         !c->hip_ok(launch_fmt_convert(c->cond_f, R, c->CD, c->CDp, c->cond_a, c->cemb.f16, st), "cond"))
         return -1;
-    if (!enqueue_forward(c, t)) return -1;
+    if (!enqueue_cond_embed(c) || !enqueue_forward(c, t)) return -1;
     if (!c->hip_ok(hipMemcpyAsync(v_out, c->v, (size_t) R * D * 4, hipMemcpyDeviceToHost, st), "v") ||
         !c->hip_ok(hipStreamSynchronize(st), "forward sync"))
         return -1;
@@ -542,6 +546,7 @@ int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const f
         return -1;
     // torch linspace(0, 1, nfe) in f32 (src/pipeline.cpp:12-13)
     auto ode_t = [&](int i) { return (float) ((double) i / (double) (g.nfe - 1)); };
+    if (!enqueue_cond_embed(c)) return -1;
     for (int s = 0; s < g.nfe - 1; s++) {
         if (!enqueue_forward(c, ode_t(s))) return -1;
         const float dt = ode_t(s + 1) - ode_t(s);
