@@ -305,8 +305,9 @@ def main():
     ap.add_argument("--ftype", default="f16", choices=["f16", "f32"])
     ap.add_argument("--workload", default="iid", choices=["iid", "smooth", "stress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--lanes", type=int, default=2, choices=[1, 2],
-                    help="1: every launch chain on one stream (kernel traces comparable with the per-stage events)")
+    ap.add_argument("--lanes", type=int, default=3, choices=[1, 3],
+                    help="3: the library's own lanes (consecutive batches overlap); 1: every launch chain on "
+                         "one stream (kernel traces comparable with the per-stage events)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run the 256 MiB calibration copy (for counter runs)")
     args = ap.parse_args()

@@ -71,10 +71,11 @@ def test_decode_paths_agree(om, torch_cuda):
     assert np.array_equal(out.cpu().numpy(), full)
 
 
-def test_two_lane_device_decodes(om, torch_cuda):
-    """device decodes on the library's own stream alternate between two
-    lanes (consecutive batches overlap on the GPU): every batch equals the
-    host path bit for bit, the ragged last one included"""
+def test_multi_lane_device_decodes(om, torch_cuda):
+    """device decodes on the library's own stream rotate over the decoder's
+    lanes (consecutive batches overlap on the GPU; four batches reach every
+    lane and reuse the first): every batch equals the host path bit for bit,
+    the ragged last one included"""
     torch = torch_cuda
     _, dec, lat = _decoders(om, "f16", SMALL_IC, SMALL_OC, 7, 2)
     starts = range(0, 7, 2)
