@@ -321,7 +321,6 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
     const int IC = p.IC, H = p.H, W = p.W;
     const int K = 9 * IC;
     const int HW = H * W;
-    const int kpt = IC / BK;
     const int fr = n0 / HW;
     const int T = p.T;
 
@@ -498,7 +497,6 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
     const int y0 = ty * HR_TH, x0 = (trem - ty * tiles_x) * HR_TW;
     const int m0 = mt * BM;
     const int IC = p.IC, H = p.H, W = p.W;
-    const int K = 9 * IC;
     const int NC = IC / BK, T = 9 * NC;
 
     // A DMA: instruction j of a wave moves the 16-row block g = m0/16 +

@@ -343,7 +343,6 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     if (tid < BN) {
         const int p = tid;
         const int pix = tile_pix<TWC>(pix0, r, p);
-        const int y = pix / r, x = pix - y * r;
         float fl[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < C; c += 4) {
