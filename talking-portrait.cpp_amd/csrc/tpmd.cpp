@@ -121,12 +121,12 @@ struct tpmd_ctx {
 
     bool profile = false;
 
-    // frame streaming (tpmd_decode_frames): two device frame slots, pinned
-    // host staging, a copy stream and events; made by the first call
+    // frame streaming (tpmd_decode_frames): one device frame slot per lane,
+    // pinned host staging, a copy stream and events; made by the first call
     struct {
         hipStream_t copy = nullptr;
-        hipEvent_t computed[2] = {}, copied[2] = {};
-        void *dev[2] = {}, *host[2] = {};
+        hipEvent_t computed[kLanes] = {}, copied[kLanes] = {};
+        void *dev[kLanes] = {}, *host[kLanes] = {};
         size_t bytes = 0;  // per slot
     } fs;
     std::vector<hipEvent_t> ev;
@@ -207,7 +207,7 @@ struct tpmd_ctx {
         for (void *p : batch_allocs) (void) hipFree(p);
         for (void *p : scr)
             if (p) (void) hipFree(p);
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < kLanes; i++) {
             if (fs.dev[i]) (void) hipFree(fs.dev[i]);
             if (fs.host[i]) (void) hipHostFree(fs.host[i]);
             if (fs.computed[i]) (void) hipEventDestroy(fs.computed[i]);
@@ -983,19 +983,19 @@ static bool frame_slots(tpmd_ctx *c, size_t bytes) {
     auto &f = c->fs;
     if (!f.copy) {
         if (!c->hip_ok(hipStreamCreateWithFlags(&f.copy, hipStreamNonBlocking), "copy stream")) return false;
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < tpmd_ctx::kLanes; i++)
             if (!c->hip_ok(hipEventCreateWithFlags(&f.computed[i], hipEventDisableTiming), "event") ||
                 !c->hip_ok(hipEventCreateWithFlags(&f.copied[i], hipEventDisableTiming), "event"))
                 return false;
     }
     if (f.bytes >= bytes) return true;
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < tpmd_ctx::kLanes; i++) {
         if (f.dev[i]) (void) hipFree(f.dev[i]);
         if (f.host[i]) (void) hipHostFree(f.host[i]);
         f.dev[i] = f.host[i] = nullptr;
     }
     f.bytes = 0;
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < tpmd_ctx::kLanes; i++) {
         if (!c->hip_ok(hipMalloc(&f.dev[i], bytes), "frame slot") ||
             !c->hip_ok(hipHostMalloc(&f.host[i], bytes, hipHostMallocDefault), "pinned frame slot"))
             return false;
@@ -1025,9 +1025,15 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
     auto &f = c->fs;
     const int64_t nb = (n_frames + B - 1) / B;
     bool ok = true, stopped = false;
+    // on the library's own stream, batch k runs on lane k % kLanes (its own
+    // buffers and stream) with frame slot k % kLanes; on a caller's stream,
+    // every batch runs on lane 0 in that stream
+    constexpr int NS = tpmd_ctx::kLanes;
+    const bool multi = c->stream == c->own_stream;
+    hipStream_t keep = c->stream;
     // frames of batch k, from its pinned slot, to the caller
     auto deliver = [&](int64_t k) {
-        const int s = (int) (k & 1);
+        const int s = (int) (k % NS);
         const int64_t t0 = k * B;
         const int64_t nk = std::min<int64_t>(B, n_frames - t0);
         if (!c->hip_ok(hipEventSynchronize(f.copied[s]), "frame copy")) return ok = false;
@@ -1039,11 +1045,14 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
         return true;
     };
     for (int64_t k = 0; k < nb && ok && !stopped; k++) {
-        const int s = (int) (k & 1);
+        const int s = (int) (k % NS);
         const int64_t t0 = k * B;
         const int nk = (int) std::min<int64_t>(B, n_frames - t0);
-        // slot s is free once the copy of batch k-2 has finished
-        if (k >= 2 && !c->hip_ok(hipStreamWaitEvent(c->stream, f.copied[s], 0), "wait")) ok = false;
+        const int li = multi ? s : 0;
+        c->L = &c->lane[li];
+        c->stream = li == 0 ? keep : c->lane_stream[li];
+        // slot s is free once the copy of batch k-NS has finished
+        if (k >= NS && !c->hip_ok(hipStreamWaitEvent(c->stream, f.copied[s], 0), "wait")) ok = false;
         ok = ok && c->hip_ok(hipMemcpyAsync(c->L->lat, styles + (size_t) t0 * 512, (size_t) nk * 512 * 4,
                                             hipMemcpyHostToDevice, c->stream),
                              "style upload");
@@ -1058,11 +1067,15 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
              c->hip_ok(hipMemcpyAsync(f.host[s], f.dev[s], (size_t) nk * fsz, hipMemcpyDeviceToHost, f.copy),
                        "frame download") &&
              c->hip_ok(hipEventRecord(f.copied[s], f.copy), "event");
+        c->L = &c->lane[0];
+        c->stream = keep;
         if (ok && k >= 1) deliver(k - 1);  // batch k decodes while batch k-1 is handed over
         if (ok && !stopped && k == nb - 1) deliver(k);
     }
-    // leave both streams idle: the slots may be reused by the next call
-    const bool drained = c->hip_ok(hipStreamSynchronize(f.copy), "drain") &&
+    c->L = &c->lane[0];
+    c->stream = keep;
+    // leave every stream idle: the slots may be reused by the next call
+    const bool drained = c->hip_ok(hipStreamSynchronize(f.copy), "drain") && drain_lanes(c) &&
                          c->hip_ok(hipStreamSynchronize(c->stream), "drain");
     c->profile = prof;
     return ok && drained ? n_frames : -1;
