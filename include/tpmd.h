@@ -125,17 +125,18 @@ int tpmd_set_feats_device(tpmd_ctx *ctx, const float *const *feats_dev);
 int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, int on_device);
 /* Frame output path of a clip (the generation loop's decode stage,
  * src/pipeline.cpp:160-185): n_frames latents (host [n][512]) are decoded
- * in launches of `batch` frames; while launch k runs, the frames of launch
- * k-1 come back over a second stream into pinned staging and are handed
- * over.  format TPMD_FRAME_F32: [3][R][R] f32 per frame, as decode_batch;
+ * in launches of `batch` frames (rotating over the decoder's lanes when it
+ * runs on its own stream); while launch k runs, the frames of launch k-1
+ * come back over a copy stream into pinned staging and are handed over.  format TPMD_FRAME_F32: [3][R][R] f32 per frame, as decode_batch;
  * TPMD_FRAME_RGB24: [R][R][3] u8 per frame, converted on the GPU with the
  * video writer's rule (tools/tp-cli.cpp:43-53: clamp to [-1,1],
  * (v+1)/2*255, truncate), a quarter of the bytes.  out: host buffer for all
  * frames, or NULL; cb: called per frame in order with the frame (valid only
  * during the call, tp_frame_cb semantics, include/tp.h:57-62), or NULL;
  * a nonzero return stops decoding.  Returns n_frames (also when stopped, as
- * generate_impl does) or -1.  The first call allocates two slots of device
- * and pinned host memory for `batch` frames, kept by the context. */
+ * generate_impl does) or -1.  The first call allocates one slot of device
+ * and one of pinned host memory per lane (three) for `batch` frames, kept
+ * by the context. */
 #define TPMD_FRAME_F32 0
 #define TPMD_FRAME_RGB24 1
 typedef int (*tpmd_frame_cb)(int64_t frame_idx, const void *frame, void *ud);
