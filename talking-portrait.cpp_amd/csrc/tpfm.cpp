@@ -78,6 +78,7 @@ struct tpfm_ctx {
     bool t0_16 = false, t2_16 = false;
     float *pos = nullptr;
     std::vector<float> t_freqs;
+    std::vector<float> h_cond, h_x60;  // sample_chunk's host staging (sized at prepare)
 
     // activations
     float *tfk = nullptr, *tf = nullptr, *te0 = nullptr, *te = nullptr;
@@ -483,6 +484,8 @@ int tpfm_prepare(tpfm_ctx *c) {
         }
         c->ws = F(wsn);
     }
+    c->h_cond.assign((size_t) 3 * T * c->CD, 0.0f);
+    c->h_x60.assign((size_t) T * g.dim_w, 0.0f);
     if (!c->tf || !c->tfk || !c->te0 || !c->te || !c->cond_f || !c->cond_a || !c->clin || !c->sc_a || !c->x60 || !c->x60_a ||
         !c->x1 || !c->x || !c->mod || !c->h_a || !c->qkv || !c->o_a || !c->m1_a || !c->v || !c->ws)
         return -1;
@@ -527,7 +530,10 @@ int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const f
         return -1;
     }
     // condition rows [wr | wa | we] per branch and frame (src/pipeline.cpp:22-36)
-    std::vector<float> cond((size_t) 3 * T * CD, 0.0f), x60((size_t) T * D);
+    // (host staging kept by the context: a chunk allocates nothing)
+    std::vector<float> &cond = c->h_cond, &x60 = c->h_x60;
+    cond.assign((size_t) 3 * T * CD, 0.0f);
+    x60.resize((size_t) T * D);
     for (int b = 0; b < 3; b++)
         for (int f = 0; f < T; f++) {
             float *row = cond.data() + ((size_t) b * T + f) * CD;

@@ -19,6 +19,10 @@
 #include <cstring>
 #include <map>
 #include <new>
+#include <atomic>
+#include <condition_variable>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -35,6 +39,78 @@ const int REF_OC[7] = {512, 512, 512, 256, 128, 64, 32};
 struct HostTensor {
     std::vector<float> data;  // scale-folded f32
     int flags = 0;
+};
+
+// helper threads for the frame path's host copies out of the pinned slots
+// (one thread copies ~5-10 GB/s, less than the decoder produces frames):
+// made by the first tpmd_decode_frames call and kept by the context, so later
+// calls allocate nothing; a copy is split in parts that the helpers and the
+// calling thread take in turn
+struct CopyPool {
+    std::vector<std::thread> th;
+    std::mutex m;
+    std::condition_variable go, done;
+    char *dst = nullptr;
+    const char *src = nullptr;
+    size_t bytes = 0, part = 0;
+    int nparts = 0, finished = 0;
+    std::atomic<int> next{0};
+    unsigned gen = 0;
+    bool quit = false;
+
+    explicit CopyPool(int n) {
+        for (int i = 0; i < n; i++) th.emplace_back([this] { loop(); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(m);
+            quit = true;
+        }
+        go.notify_all();
+        for (auto &t : th) t.join();
+    }
+    void work() {
+        for (;;) {
+            const int i = next.fetch_add(1);
+            if (i >= nparts) return;
+            const size_t b0 = (size_t) i * part;
+            memcpy(dst + b0, src + b0, std::min(part, bytes - b0));
+        }
+    }
+    void loop() {
+        unsigned seen = 0;
+        std::unique_lock<std::mutex> lk(m);
+        for (;;) {
+            go.wait(lk, [&] { return quit || gen != seen; });
+            if (quit) return;
+            seen = gen;
+            lk.unlock();
+            work();
+            lk.lock();
+            if (++finished == (int) th.size()) done.notify_one();
+        }
+    }
+    void copy(char *d, const char *s_, size_t n) {
+        if (th.empty() || n < ((size_t) 2 << 20)) {
+            memcpy(d, s_, n);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(m);
+            dst = d;
+            src = s_;
+            bytes = n;
+            part = (n / (th.size() + 1) + 4095) & ~(size_t) 4095;
+            nparts = (int) ((n + part - 1) / part);
+            next = 0;
+            finished = 0;
+            ++gen;
+        }
+        go.notify_all();
+        work();
+        std::unique_lock<std::mutex> lk(m);
+        done.wait(lk, [&] { return finished == (int) th.size(); });
+    }
 };
 
 struct ConvW {
@@ -128,6 +204,7 @@ struct tpmd_ctx {
         hipEvent_t computed[kLanes] = {}, copied[kLanes] = {};
         void *dev[kLanes] = {}, *host[kLanes] = {};
         size_t bytes = 0;  // per slot
+        std::unique_ptr<CopyPool> pool;
     } fs;
     std::vector<hipEvent_t> ev;
     std::vector<float> times;
@@ -958,27 +1035,6 @@ static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *img
 }
 
 // slot buffers of the frame stream, grow-only
-// host copy of a batch of frames from its pinned slot into the caller's
-// (pageable) buffer, split over up to 8 threads: one thread copies ~5-10 GB/s,
-// less than the decoder produces frames
-static void frames_memcpy(char *dst, const char *src, size_t bytes) {
-    const unsigned hw = std::thread::hardware_concurrency();
-    const size_t nt = std::min<size_t>({8, hw ? hw : 1, bytes / (1u << 20) + 1});
-    if (nt <= 1) {
-        memcpy(dst, src, bytes);
-        return;
-    }
-    const size_t part = (bytes / nt + 4095) & ~(size_t) 4095;
-    std::vector<std::thread> th;
-    th.reserve(nt - 1);
-    for (size_t i = 1; i < nt && i * part < bytes; i++) {
-        const size_t b0 = i * part, n = std::min(part, bytes - b0);
-        th.emplace_back([=]() { memcpy(dst + b0, src + b0, n); });
-    }
-    memcpy(dst, src, std::min(part, bytes));
-    for (auto &t : th) t.join();
-}
-
 static bool frame_slots(tpmd_ctx *c, size_t bytes) {
     auto &f = c->fs;
     if (!f.copy) {
@@ -987,6 +1043,14 @@ static bool frame_slots(tpmd_ctx *c, size_t bytes) {
             if (!c->hip_ok(hipEventCreateWithFlags(&f.computed[i], hipEventDisableTiming), "event") ||
                 !c->hip_ok(hipEventCreateWithFlags(&f.copied[i], hipEventDisableTiming), "event"))
                 return false;
+    }
+    if (!f.pool) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        f.pool.reset(new (std::nothrow) CopyPool((int) std::min(7u, hw > 1 ? hw - 1 : 0u)));
+        if (!f.pool) {
+            c->err = "frame copy threads: out of memory";
+            return false;
+        }
     }
     if (f.bytes >= bytes) return true;
     for (int i = 0; i < tpmd_ctx::kLanes; i++) {
@@ -1038,7 +1102,7 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
         const int64_t nk = std::min<int64_t>(B, n_frames - t0);
         if (!c->hip_ok(hipEventSynchronize(f.copied[s]), "frame copy")) return ok = false;
         const char *src = (const char *) f.host[s];
-        if (out) frames_memcpy((char *) out + (size_t) t0 * fsz, src, (size_t) nk * fsz);
+        if (out) f.pool->copy((char *) out + (size_t) t0 * fsz, src, (size_t) nk * fsz);
         if (cb)
             for (int64_t i = 0; i < nk; i++)
                 if (cb(t0 + i, src + (size_t) i * fsz, ud)) return !(stopped = true);
