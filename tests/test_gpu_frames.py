@@ -65,3 +65,33 @@ def test_frame_callback_stops(torch_cuda, dec):
     assert seen == list(range(6))
     # the context keeps working after a stopped stream
     assert np.array_equal(dec.decode_frames(lat[:3]), want[:3])
+
+
+def test_frames_reuse_lanes_and_slots(torch_cuda, dec):
+    """more launches than lanes: every lane and frame slot is reused (the
+    slot's previous download must finish first), frames unchanged"""
+    lat = synth.latents(30, 1002, "ar1")                 # 8 launches of 4, last one ragged
+    got = dec.decode_frames(lat)
+    want = np.concatenate([dec.decode_batch(lat[t:t + 4]) for t in range(0, 30, 4)])
+    assert np.array_equal(got, want)
+    rgb = dec.decode_frames(lat, tpmd.FRAME_RGB24)
+    assert np.array_equal(rgb, to_rgb24(want))
+
+
+def test_frames_on_caller_stream(torch_cuda):
+    """on a caller's stream every launch runs on lane 0 in that stream"""
+    torch = torch_cuda
+    raw, _, feats = synth.workload("smooth", 1, "f16", IC, OC)
+    d = tpmd.MotionDecoder("f16", len(IC), IC, OC)
+    d.set_weights(raw)
+    d.prepare()
+    d.build(4)
+    d.set_feats(feats)
+    lat = synth.latents(18, 1003, "ar1")
+    want = np.concatenate([d.decode_batch(lat[t:t + 4]) for t in range(0, 18, 4)])
+    s = torch.cuda.Stream()
+    d.use_stream(s)
+    got = d.decode_frames(lat)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want)
+    d.close()
