@@ -399,8 +399,17 @@ def main():
         t0h = time.perf_counter()
         dec.decode_frames(lat, fmt)
         host[name] = round(n_seq / (time.perf_counter() - t0h), 1)
+    # the same into pinned caller buffers, which take the downloads directly
+    for name, fmt, shape, dt in (("f32_chw_pinned", tpmd.FRAME_F32, (n_seq, 3, 512, 512), torch.float32),
+                                 ("rgb24_pinned", tpmd.FRAME_RGB24, (n_seq, 512, 512, 3), torch.uint8)):
+        buf = torch.empty(shape, dtype=dt, pin_memory=True)
+        dec.decode_frames(lat, fmt, out=buf)              # warm
+        t0h = time.perf_counter()
+        dec.decode_frames(lat, fmt, out=buf)
+        host[name] = round(n_seq / (time.perf_counter() - t0h), 1)
+        del buf
     out["host_delivered_fps"] = {"frames": n_seq, **host,
-                                 "note": "pageable host buffer, PCIe download included"}
+                                 "note": "host buffers (pageable, or pinned where named), PCIe download included"}
     out["encoder"] = encoder_timing(args.ftype)
     out["fmt"] = fmt_timing(args.ftype)
     out["gather"] = gather_timing()

@@ -131,7 +131,9 @@ int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, in
  * TPMD_FRAME_RGB24: [R][R][3] u8 per frame, converted on the GPU with the
  * video writer's rule (tools/tp-cli.cpp:43-53: clamp to [-1,1],
  * (v+1)/2*255, truncate), a quarter of the bytes.  out: host buffer for all
- * frames, or NULL; cb: called per frame in order with the frame (valid only
+ * frames, or NULL (pinned memory, e.g. from hipHostMalloc, takes the
+ * downloads directly; pageable memory is filled from pinned staging by
+ * helper threads); cb: called per frame in order with the frame (valid only
  * during the call, tp_frame_cb semantics, include/tp.h:57-62), or NULL;
  * a nonzero return stops decoding.  Returns n_frames (also when stopped, as
  * generate_impl does) or -1.  The first call allocates one slot of device

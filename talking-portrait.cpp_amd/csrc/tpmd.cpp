@@ -1095,14 +1095,21 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
     constexpr int NS = tpmd_ctx::kLanes;
     const bool multi = c->stream == c->own_stream;
     hipStream_t keep = c->stream;
+    // a pinned caller buffer takes the downloads directly (no staging copy)
+    bool direct = false;
+    if (out) {
+        hipPointerAttribute_t pa{};
+        direct = hipPointerGetAttributes(&pa, out) == hipSuccess && pa.type == hipMemoryTypeHost;
+        (void) hipGetLastError();  // a pageable buffer is reported as an error: clear it
+    }
     // frames of batch k, from its pinned slot, to the caller
     auto deliver = [&](int64_t k) {
         const int s = (int) (k % NS);
         const int64_t t0 = k * B;
         const int64_t nk = std::min<int64_t>(B, n_frames - t0);
         if (!c->hip_ok(hipEventSynchronize(f.copied[s]), "frame copy")) return ok = false;
-        const char *src = (const char *) f.host[s];
-        if (out) f.pool->copy((char *) out + (size_t) t0 * fsz, src, (size_t) nk * fsz);
+        const char *src = direct ? (const char *) out + (size_t) t0 * fsz : (const char *) f.host[s];
+        if (out && !direct) f.pool->copy((char *) out + (size_t) t0 * fsz, src, (size_t) nk * fsz);
         if (cb)
             for (int64_t i = 0; i < nk; i++)
                 if (cb(t0 + i, src + (size_t) i * fsz, ud)) return !(stopped = true);
@@ -1128,7 +1135,8 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
         }
         ok = ok && c->hip_ok(hipEventRecord(f.computed[s], c->stream), "event") &&
              c->hip_ok(hipStreamWaitEvent(f.copy, f.computed[s], 0), "wait") &&
-             c->hip_ok(hipMemcpyAsync(f.host[s], f.dev[s], (size_t) nk * fsz, hipMemcpyDeviceToHost, f.copy),
+             c->hip_ok(hipMemcpyAsync(direct ? (char *) out + (size_t) t0 * fsz : f.host[s], f.dev[s],
+                                      (size_t) nk * fsz, hipMemcpyDeviceToHost, f.copy),
                        "frame download") &&
              c->hip_ok(hipEventRecord(f.copied[s], f.copy), "event");
         c->L = &c->lane[0];

@@ -240,21 +240,30 @@ class MotionDecoder:
         n = styles_dev.shape[0]
         self._check(lib().tpmd_decode_batch(self.h, _ptr(styles_dev), n, _ptr(imgs_dev), 1))
 
-    def decode_frames(self, styles, fmt=FRAME_F32, to_buffer=True, cb=None):
+    def decode_frames(self, styles, fmt=FRAME_F32, to_buffer=True, cb=None, out=None):
         """a clip of latents (n, 512) through tpmd_decode_frames: returns the
         frames array (n, 3, R, R) f32 or (n, R, R, 3) u8 when to_buffer, and
-        calls cb(index, frame_array) per frame (a truthy return stops)"""
+        calls cb(index, frame_array) per frame (a truthy return stops).  out:
+        a caller's host buffer of that shape and type (a numpy array, or a
+        torch CPU tensor, pinned or not) to fill instead"""
         s = np.ascontiguousarray(styles, dtype=np.float32).reshape(-1, 512)
         n, R = s.shape[0], self.res
         shape, dt = ((3, R, R), np.float32) if fmt == FRAME_F32 else ((R, R, 3), np.uint8)
-        out = np.empty((n,) + shape, dt) if to_buffer else None
+        if out is not None:
+            nb = out.numel() * out.element_size() if hasattr(out, "numel") else out.nbytes
+            if nb != n * int(np.prod(shape)) * np.dtype(dt).itemsize:
+                raise TpmdError("decode_frames: out has the wrong size")
+            optr = out.data_ptr() if hasattr(out, "data_ptr") else _hptr(out)
+        else:
+            out = np.empty((n,) + shape, dt) if to_buffer else None
+            optr = _hptr(out) if out is not None else None
         nbytes = int(np.prod(shape)) * np.dtype(dt).itemsize
 
         def tramp(idx, ptr, ud):
             buf = (ctypes.c_char * nbytes).from_address(ptr)
             return 1 if cb(idx, np.frombuffer(buf, dt).reshape(shape).copy()) else 0
         c_cb = FRAME_CB(tramp) if cb else None
-        rc = lib().tpmd_decode_frames(self.h, _hptr(s), n, fmt, _hptr(out) if out is not None else None,
+        rc = lib().tpmd_decode_frames(self.h, _hptr(s), n, fmt, optr,
                                       ctypes.cast(c_cb, ctypes.c_void_p) if c_cb else None, None)
         if rc < 0:
             raise TpmdError(self.last_error)

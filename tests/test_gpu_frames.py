@@ -95,3 +95,26 @@ def test_frames_on_caller_stream(torch_cuda):
     torch.cuda.synchronize()
     assert np.array_equal(got, want)
     d.close()
+
+
+def test_frames_into_caller_buffers(torch_cuda, dec):
+    """a pinned caller buffer takes the downloads directly, a pageable one is
+    filled from the pinned staging; both hold decode_batch's frames, and the
+    callback sees the same frames"""
+    torch = torch_cuda
+    lat = synth.latents(14, 1004, "ar1")
+    want = np.concatenate([dec.decode_batch(lat[t:t + 4]) for t in range(0, 14, 4)])
+    for pinned in (True, False):
+        buf = torch.empty((14, 3, 512, 512), dtype=torch.float32, pin_memory=pinned)
+        seen = []
+
+        def cb(i, frame):
+            seen.append(i)
+            assert np.array_equal(frame, want[i])
+            return False
+        dec.decode_frames(lat, cb=cb, out=buf)
+        assert seen == list(range(14))
+        assert np.array_equal(buf.numpy(), want)
+    rgb = torch.empty((14, 512, 512, 3), dtype=torch.uint8, pin_memory=True)
+    dec.decode_frames(lat, tpmd.FRAME_RGB24, out=rgb)
+    assert np.array_equal(rgb.numpy(), to_rgb24(want))
