@@ -135,22 +135,34 @@ __global__ __launch_bounds__(256) void fmt_attn_kernel(const float *__restrict__
 #pragma unroll
     for (int k = 0; k < MAXD; k++) q[k] = lane + 64 * k < hd ? qr[lane + 64 * k] : 0.0f;
     const int k0 = tq - w > 0 ? tq - w : 0, k1 = tq + w < T - 1 ? tq + w : T - 1;
-    float sc[MAXK];
-    float mx = -INFINITY;
+    // every key and value row of the band is requested before any is used,
+    // and the 2w+1 dot products are reduced together (independent chains)
+    float kv[MAXK][MAXD], vv[MAXK][MAXD];
 #pragma unroll
     for (int j = 0; j < MAXK; j++) {
-        sc[j] = -INFINITY;
-        const int tk = k0 + j;
-        if (tk <= k1) {
-            const float *kr = qkv + ((int64_t) b * T + tk) * rs + H + hh * hd;
-            float a = 0.0f;
+        const int tk = k0 + j <= k1 ? k0 + j : k1;
+        const float *kr = qkv + ((int64_t) b * T + tk) * rs + H + hh * hd;
+        const float *vr = kr + H;
 #pragma unroll
-            for (int k = 0; k < MAXD; k++)
-                if (lane + 64 * k < hd) a = __builtin_fmaf(q[k], kr[lane + 64 * k], a);
-            sc[j] = group_sum<64>(a) * scale;
-            mx = sc[j] > mx ? sc[j] : mx;
+        for (int k = 0; k < MAXD; k++) {
+            kv[j][k] = lane + 64 * k < hd ? kr[lane + 64 * k] : 0.0f;
+            vv[j][k] = lane + 64 * k < hd ? vr[lane + 64 * k] : 0.0f;
         }
     }
+    float sc[MAXK];
+#pragma unroll
+    for (int j = 0; j < MAXK; j++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MAXD; k++) a = __builtin_fmaf(q[k], kv[j][k], a);
+        sc[j] = a;
+    }
+#pragma unroll
+    for (int j = 0; j < MAXK; j++) sc[j] = group_sum<64>(sc[j]) * scale;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MAXK; j++)
+        if (k0 + j <= k1) mx = sc[j] > mx ? sc[j] : mx;
     float den = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXK; j++) {
@@ -160,12 +172,9 @@ __global__ __launch_bounds__(256) void fmt_attn_kernel(const float *__restrict__
     float acc[MAXD] = {};
 #pragma unroll
     for (int j = 0; j < MAXK; j++) {
-        const int tk = k0 + j;
-        if (tk <= k1) {
-            const float *vr = qkv + ((int64_t) b * T + tk) * rs + 2 * H + hh * hd;
+        if (k0 + j <= k1) {
 #pragma unroll
-            for (int k = 0; k < MAXD; k++)
-                if (lane + 64 * k < hd) acc[k] = __builtin_fmaf(sc[j], vr[lane + 64 * k], acc[k]);
+            for (int k = 0; k < MAXD; k++) acc[k] = __builtin_fmaf(sc[j], vv[j][k], acc[k]);
         }
     }
     TO *orow = o + ((int64_t) b * T + tq) * H + hh * hd;
