@@ -11,7 +11,7 @@
 //     by one ds_read_b128 per lane), so it holds no registers.  FRAG: A is
 //     stored in that order (A_ORDER_FRAG), so each fragment's DMA reads
 //     1 KB of contiguous memory instead of 32 bytes of 32 rows;
-//   * wave w computes rows w*TH/4 .. of the block: for each tap (dy, dx) and
+//   * wave w computes rows w*RPW .. of the block (RPW = 2): for each tap (dy, dx) and
 //     16-channel step, the B fragment is the halo row shifted by (dy, dx);
 //   * the activated tile goes to LDS over the halo and the two-phase stage
 //     tail of tpmd_tail.h runs on it (the tail's skips and the folded ToFlow
@@ -21,32 +21,50 @@
 
 namespace tpmd {
 
-template <int TH>
+// FG (the stage's warp feeds ToRGB alone, TailArgs::featg): each lane finishes
+// its own pixel from the accumulators (the ToFlow dot in registers, halves
+// joined across the two 32-lane halves), so the activated tile never goes to
+// LDS and the workgroup needs only the halo, A and the ToFlow weights;
+// F32_SWZ: 64-byte halo pixels, the 16-byte chunk index XORed with bits 2-3
+// of the pixel index (16 consecutive pixels' reads of one chunk still hit
+// distinct banks) instead of a 16-byte pad per pixel.
+// Measured on MI355X, r512 at 16 frames (FG): 8 x 32 blocks of 4 waves,
+// three per CU, 222 us; the same with F32_SWZ (four per CU) 184 us;
+// 16 x 32 blocks of 8 waves (two per CU: A loaded once per 512 pixels, 18
+// halo rows per 16) 175 us, 183 us with F32_SWZ.  The non-FG form keeps the
+// same blocks (its activated tile takes 90 KB of LDS: one per CU).
+constexpr int F32_NT = 512;
+constexpr bool F32_SWZ = false;
+
+template <int TH, bool FG = false>
 struct fused32_cfg {
-    static constexpr int C = 32, NT = 256, TW = 32, BN = TH * TW;
+    static constexpr int C = 32, NT = F32_NT, TW = 32, BN = TH * TW;
     static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
-    static constexpr int PXB = C * 2 + 16;              // padded halo pixel (bytes)
+    static constexpr bool SWZ = FG && F32_SWZ;
+    static constexpr int PXB = SWZ ? C * 2 : C * 2 + 16;  // halo pixel (bytes)
     static constexpr int CPP = C * 2 / 16;              // 16-byte chunks per pixel
     static constexpr int HCH = HPX * CPP;
     static constexpr int PF = (HCH + NT - 1) / NT;      // halo chunks per thread
     static constexpr int KS = C / 16;                   // MFMA k steps per tap
     static constexpr int NAF = 9 * KS;                  // A fragments
-    static constexpr int RPW = TH / 4;                  // output rows per wave
+    static constexpr int RPW = TH / (NT / 64);          // output rows per wave
     typedef tile_tail_lds<C, BN> L;
     static constexpr int HALO = HPX * PXB;
     static constexpr int AOFF = (HALO + 255) / 256 * 256;  // A fragments, fragment-major
     static constexpr int CONV = AOFF + NAF * 1024;          // conv-phase LDS
-    static constexpr int TAIL = L::WFS0 * 4;                // so + prm, over the conv's LDS
+    static constexpr int TAIL = FG ? 0 : L::WFS0 * 4;       // so + prm, over the conv's LDS
     static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
-    static_assert(TH % 4 == 0, "rows per wave");
+    static_assert(TH % (NT / 64) == 0 && (FG ? BN == NT : BN % NT == 0), "rows per wave");
+    static_assert(!FG || RPW == 2, "FG: a lane's two block rows are its pixel and its partner's");
+    __device__ static int hoff(int px, int c) { return px * PXB + (SWZ ? (c ^ ((px >> 2) & 3)) : c) * 16; }
 };
 
-template <typename TF, typename TT, int TH, bool FRAG>
-__global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
-                                                          int tiles_frame) {
+template <typename TF, typename TT, int TH, bool FRAG, bool FG>
+__global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
+                                                             int tiles_frame) {
     typedef half_t TA;
-    typedef fused32_cfg<TH> F;
+    typedef fused32_cfg<TH, FG> F;
     typedef typename F::L L;
     constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
     constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, NAF = F::NAF, RPW = F::RPW;
@@ -96,7 +114,7 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         const int ch = tid + i * NT;
         if (ch < HCH) {
             const int px = ch / CPP, c = ch - px * CPP;
-            *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
+            *(u32x4 *) (smem + F::hoff(px, c)) = hv[i];
         }
     });
     tile_tail_wfs_store<C, NT>(wfs, tid, wr);
@@ -113,17 +131,58 @@ __global__ __launch_bounds__(256) void conv32_tail_kernel(ConvParams p, TailArgs
         static_for<KS>([&](auto ks) {
             static_for<RPW>([&](auto b) {
                 const int hrow = wid * RPW + b + dy;
-                const u32x4 bf =
-                    *(const u32x4 *) (smem + (hrow * HWD + lrow + dx) * PXB + (ks * 2 + khalf) * 16);
+                const u32x4 bf = *(const u32x4 *) (smem + F::hoff(hrow * HWD + lrow + dx, ks * 2 + khalf));
                 const u32x4 af = *(const u32x4 *) (smem + F::AOFF + (tap * KS + ks) * 1024 + lane * 16);
                 mfma_op<TA>::run(af, bf, acc[b]);
             });
         });
         __builtin_amdgcn_sched_barrier(0);  // bound the fragments in flight (registers)
     });
-    __syncthreads();  // halo reads done: the LDS becomes the activated tile
 
     // accumulator (b, v): channel (v/4)*8 + (lane/32)*4 + v%4, tile pixel (wid*RPW + b)*32 + lane%32
+    if constexpr (FG) {
+        // ToFlow dot over this lane's 16 channels of both block rows (the
+        // c % 8 < 4 chain of the tile tail for khalf 0, the other for
+        // khalf 1, same order); the lane keeps row khalf (tile pixel
+        // wid*64 + lane = tid, whose skips it holds) and trades the other
+        // row's sum with lane ^ 32
+        float part[RPW][3];
+        static_for<RPW>([&](auto b) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) part[b][k] = 0.0f;
+        });
+        static_for<4>([&](auto i) {
+            const int row = i * 8 + khalf * 4;
+            const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * C + row);
+            const floatx4 bb = *(const floatx4 *) (p.bias + row);
+            floatx4 w[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++) w[k] = *(const floatx4 *) (wfs + k * C + row);
+            static_for<RPW>([&](auto b) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float v = leaky(acc[b][i * 4 + j] * id[j] + bb[j]);
+#pragma unroll
+                    for (int k = 0; k < 3; k++) part[b][k] = __builtin_fmaf(w[k][j], v, part[b][k]);
+                }
+            });
+        });
+        float fl[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const float mine = khalf ? part[1][k] : part[0][k];
+            const float give = khalf ? part[0][k] : part[1][k];
+            const float got = __shfl_xor(give, 32);
+            fl[k] = khalf ? got + mine : mine + got;
+        }
+        const int pix = tile_pix<TW>(n0 - fr * (H * W), W, tid);
+        taps4 t;
+        float m;
+        tail_flow_head(ta, fl, fr, pix, sk, t, m);
+        tail_featg_rgb(ta, t, m, fr, pix, sk);
+        return;
+    }
+    __syncthreads();  // halo reads done: the LDS becomes the activated tile
     static_for<RPW>([&](auto b) {
         const int col = (wid * RPW + b) * TW + lrow;
         static_for<4>([&](auto i) {
@@ -312,13 +371,19 @@ bool modconv_fused32_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 3
 
 hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
                                   hipStream_t st) {
-    constexpr int TH = 8;
+    constexpr int TH = 16;
     if (p.IC != 32 || p.OC != 32 || p.M != 32 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
-#define TPMD_L(TT, FR) \
-    hipLaunchKernelGGL((conv32_tail_kernel<half_t, TT, TH, FR>), grid, dim3(256), 0, st, p, ta, tiles_x, tiles_frame)
+#define TPMD_L2(TT, FR, FG) \
+    hipLaunchKernelGGL((conv32_tail_kernel<half_t, TT, TH, FR, FG>), grid, dim3(F32_NT), 0, st, p, ta, tiles_x, \
+                       tiles_frame)
+#define TPMD_L(TT, FR)                               \
+    do {                                             \
+        if (ta.featg) TPMD_L2(TT, FR, true);         \
+        else TPMD_L2(TT, FR, false);                 \
+    } while (0)
     if (trunk_f16) {
         if (frag) TPMD_L(half_t, true);
         else TPMD_L(half_t, false);
@@ -327,6 +392,7 @@ hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool 
         else TPMD_L(float, false);
     }
 #undef TPMD_L
+#undef TPMD_L2
     return hipGetLastError();
 }
 

@@ -325,6 +325,62 @@ template <> struct feat8<float> {
 
 // Runs after the activated tile `so` ([BN][SOS] f32) and `wfs` are written
 // and a barrier has made them visible; prm is [BN][PRM] scratch.
+// Phase 1 of one pixel, part 1: the ToFlow bias and skip, the flow output,
+// and the warp's sampling taps and mask (fl: the ToFlow dot, bias not added)
+__device__ __forceinline__ void tail_flow_head(const TailArgs &a, float fl[3], int fr, int pix,
+                                               const tail_skip &sk, taps4 &t, float &m) {
+#pragma clang fp contract(off)
+    const int r = a.r, RR = r * r;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        fl[k] = fl[k] + a.fbias[k];
+        if (a.flow_prev) fl[k] = fl[k] + sk.fl[k];
+    }
+    if (a.flow_cur) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) a.flow_cur[((int64_t) fr * 3 + k) * RR + pix] = fl[k];
+    }
+    const float gx = tanhf(fl[0]) + sk.lx;
+    const float gy = tanhf(fl[1]) + sk.ly;
+    m = 1.0f / (1.0f + expf(-fl[2]));
+    t = gather_geometry(gx, gy, r, r);
+}
+
+// part 2 when the warp feeds ToRGB alone (featg set): Wr . (m * sum_k w_k
+// feat_k) = m * sum_k w_k (Wr . feat_k), with Wr . feat stored per feature
+// pixel; a tap outside the map reads the zero pad after it
+__device__ __forceinline__ void tail_featg_rgb(const TailArgs &a, const taps4 &t, float m, int fr, int pix,
+                                               const tail_skip &sk) {
+#pragma clang fp contract(off)
+    const int r = a.r, RR = r * r;
+    const char *gb = (const char *) a.featg;
+    const unsigned gpad = (unsigned) RR * 16u;
+    const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) t.x0 + 1u < (unsigned) r};
+    const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) t.y0 + 1u < (unsigned) r};
+    const unsigned base = (unsigned) (t.y0 * r + t.x0) * 16u;
+    floatx4 gv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * 16);
+        gv[k] = *(const floatx4 *) (gb + (inx[k & 1] && iny[k >> 1] ? off : gpad));
+    }
+    float rgb[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float wk = tap_weight(t, k);
+#pragma unroll
+        for (int q = 0; q < 3; q++) rgb[q] = __builtin_fmaf(wk, gv[k][q], rgb[q]);
+    }
+    float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+        float v = leaky(rgb[q] * m + a.rlb[q]);
+        v = v + a.rbias[q];
+        if (a.rgb_prev) v = v + sk.rgb[q];
+        rgbf[(unsigned) (q * RR + pix)] = v;
+    }
+}
+
 template <typename TF, typename TT, int C, int BN, int NT, int TWC>
 __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, float *prm, const float *wfs,
                                           int n0, int tid, const tail_skip &sk) {
@@ -343,61 +399,34 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     if (tid < BN) {
         const int p = tid;
         const int pix = tile_pix<TWC>(pix0, r, p);
-        float fl[3] = {0.0f, 0.0f, 0.0f};
+        // ToFlow dot as two chains, over channels c with c % 8 < 4 and over
+        // the rest, each in channel order, then added: the order in which
+        // the MFMA accumulator layout leaves the channels split over a
+        // lane pair, so a kernel finishing pixels in registers gets the
+        // same bits as this one
+        float fl[3], fh[3];
 #pragma unroll
-        for (int c = 0; c < C; c += 4) {
+        for (int k = 0; k < 3; k++) fl[k] = fh[k] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; c += 8) {
             const floatx4 o = *(const floatx4 *) (so + p * L::SOS + c);
+            const floatx4 q = *(const floatx4 *) (so + p * L::SOS + c + 4);
 #pragma unroll
             for (int k = 0; k < 3; k++) {
-                fl[k] = __builtin_fmaf(wfs[k * C + c], o[0], fl[k]);
-                fl[k] = __builtin_fmaf(wfs[k * C + c + 1], o[1], fl[k]);
-                fl[k] = __builtin_fmaf(wfs[k * C + c + 2], o[2], fl[k]);
-                fl[k] = __builtin_fmaf(wfs[k * C + c + 3], o[3], fl[k]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    fl[k] = __builtin_fmaf(wfs[k * C + c + j], o[j], fl[k]);
+                    fh[k] = __builtin_fmaf(wfs[k * C + c + 4 + j], q[j], fh[k]);
+                }
             }
         }
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            fl[k] = fl[k] + a.fbias[k];
-            if (a.flow_prev) fl[k] = fl[k] + sk.fl[k];
-        }
-        if (a.flow_cur) {
-#pragma unroll
-            for (int k = 0; k < 3; k++) a.flow_cur[((int64_t) fr * 3 + k) * RR + pix] = fl[k];
-        }
-        const float gx = tanhf(fl[0]) + sk.lx;
-        const float gy = tanhf(fl[1]) + sk.ly;
-        const float m = 1.0f / (1.0f + expf(-fl[2]));
-        const taps4 t = gather_geometry(gx, gy, r, r);
+        for (int k = 0; k < 3; k++) fl[k] = fl[k] + fh[k];
+        taps4 t;
+        float m;
+        tail_flow_head(a, fl, fr, pix, sk, t, m);
         if (a.featg) {
-            // the warp feeds ToRGB alone: Wr . (m * sum_k w_k feat_k) =
-            // m * sum_k w_k (Wr . feat_k), with Wr . feat stored per feature
-            // pixel; a tap outside the map reads the zero pad after it
-            const char *gb = (const char *) a.featg;
-            const unsigned gpad = (unsigned) RR * 16u;
-            const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) t.x0 + 1u < (unsigned) r};
-            const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) t.y0 + 1u < (unsigned) r};
-            const unsigned base = (unsigned) (t.y0 * r + t.x0) * 16u;
-            floatx4 gv[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * 16);
-                gv[k] = *(const floatx4 *) (gb + (inx[k & 1] && iny[k >> 1] ? off : gpad));
-            }
-            float rgb[3] = {0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float wk = tap_weight(t, k);
-#pragma unroll
-                for (int q = 0; q < 3; q++) rgb[q] = __builtin_fmaf(wk, gv[k][q], rgb[q]);
-            }
-            float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
-#pragma unroll
-            for (int q = 0; q < 3; q++) {
-                float v = leaky(rgb[q] * m + a.rlb[q]);
-                v = v + a.rbias[q];
-                if (a.rgb_prev) v = v + sk.rgb[q];
-                rgbf[(unsigned) (q * RR + pix)] = v;
-            }
+            tail_featg_rgb(a, t, m, fr, pix, sk);
         } else {
             *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
             *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
