@@ -121,8 +121,56 @@ int tpmd_set_feats_device(tpmd_ctx *ctx, const float *const *feats_dev);
  * src/motion_dec.cpp:1190-1220): n (1..batch) latents -> n frames.
  * styles: [n][512]; imgs: [n][3][R][R]; both host pointers
  * (on_device = 0, synchronous like the reference) or device pointers
- * (on_device = 1; enqueued on the decoder's stream, see tpmd_sync). */
+ * (on_device = 1, asynchronous).
+ *
+ * Device-resident calls on a caller's stream (tpmd_set_stream) are
+ * enqueued on that stream in call order.  On the decoder's own stream (the
+ * default) consecutive calls rotate over three lanes, each with its own
+ * buffers and stream, so their launch chains overlap on the GPU:
+ *   - a call reads `styles` after all work enqueued before it on HIP's null
+ *     stream (e.g. torch's default stream), and null-stream work enqueued
+ *     after the call runs after that read, so the caller may refill the
+ *     latent buffer on the null stream right away;
+ *   - a call whose `imgs` overlaps the frame buffer of an earlier call still
+ *     in flight writes its frames after that call's, so one frame buffer
+ *     may be reused: after tpmd_sync it holds the last call's frames;
+ *   - frames are complete only after tpmd_sync (latents written on another
+ *     stream need that stream synchronised first, or tpmd_set_stream). */
 int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, int on_device);
+
+/* Taps of the decode chain: device copies of the buffers that the batched
+ * decoder passes between its launches, for per-stage parity checks of the
+ * kernels exactly as decode_batch runs them.  The reference's tap plan
+ * (motion_dec::build(be, with_taps), src/motion_dec.cpp:805-883, dumped by
+ * tools/tp-parity.cpp:252-282) names its taps conv1_4, r<r>.conv1,
+ * r<r>.conv2, r<r>.flowmap, r<r>.out, r<r>.rgb; here they are the fast
+ * chain's own buffers, in its layouts (stage j: r = 8 << j, C = OC_j; the
+ * activation type is f16 in f16 mode, else f32):
+ *   TPMD_TAP_TRUNK  stage -1 (conv1 output, r = 4, C = IC_0) and
+ *                   j < n_stages - 1 (trunk, r<r>.out): CL [n][r][r][C]
+ *                   activation type, multiplied by the style of the
+ *                   up-conv that reads it;
+ *   TPMD_TAP_C1     up-conv output (r<r>.conv1): CL [n][r][r][C]
+ *                   activation type, multiplied by the dense conv's style;
+ *   TPMD_TAP_OUT    dense-conv output (r<r>.conv2): CL [n][r][r][C] f32,
+ *                   only for stages whose tail runs in a kernel of its own;
+ *   TPMD_TAP_FLOW   flow map with skip (r<r>.flowmap): SP [n][3][r][r] f32
+ *                   (the last stage stores it only while tapped);
+ *   TPMD_TAP_RGB    rgb with skip (r<r>.rgb): SP [n][3][r][r] f32, stages
+ *                   j < n_stages - 1 (the last one is the frame).
+ * tpmd_set_tap registers (dst a device buffer of `bytes`) or removes (dst
+ * NULL) one tap; every later decode_batch copies frames [0, n) of that
+ * buffer into it on the decoder's stream (a decode with taps set runs on
+ * one lane), failing if `bytes` is too small.  tpmd_tap_frame_bytes gives
+ * the bytes per frame, or -1 where the chain holds no such buffer. */
+#define TPMD_TAP_TRUNK 0
+#define TPMD_TAP_C1 1
+#define TPMD_TAP_OUT 2
+#define TPMD_TAP_FLOW 3
+#define TPMD_TAP_RGB 4
+#define TPMD_TAP_KINDS 5
+int tpmd_set_tap(tpmd_ctx *ctx, int kind, int stage, void *dst, int64_t bytes);
+int64_t tpmd_tap_frame_bytes(const tpmd_ctx *ctx, int kind, int stage);
 /* Frame output path of a clip (the generation loop's decode stage,
  * src/pipeline.cpp:160-185): n_frames latents (host [n][512]) are decoded
  * in launches of `batch` frames (rotating over the decoder's lanes when it
@@ -151,7 +199,9 @@ int tpmd_decode(tpmd_ctx *ctx, const float *style, float *img);
 int tpmd_sync(tpmd_ctx *ctx);
 /* enqueue all further work of this context on `stream` (a hipStream_t of
  * the context's device, e.g. the caller's framework stream; NULL = HIP's
- * null stream).  A new context uses a non-blocking stream of its own.  No
+ * null stream), after the work in flight on the context's streams and on
+ * the previous caller stream has finished.  A new context uses a
+ * non-blocking stream of its own.  No
  * reference counterpart: ggml owns its stream (src/backend.cpp:169-177);
  * callers that share device buffers with other stream users need this
  * ordering. */

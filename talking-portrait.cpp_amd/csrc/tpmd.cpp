@@ -190,6 +190,28 @@ struct tpmd_ctx {
     Lane *L = &lane[0];               // the lane the enqueued work uses
     hipStream_t lane_stream[kLanes] = {};  // lanes 1.. (lane 0 runs on `stream`)
     int next_lane = 0;
+    // ordering of the lanes' device-resident decodes:
+    //   ev_in[k]   recorded on the null stream as a call starts; lane k waits
+    //              for it before reading the latents (prior null-stream
+    //              writers of the latents come first)
+    //   ev_read[k] lane k has copied the call's latents; the null stream
+    //              waits for it (later null-stream writers of that buffer
+    //              come after the read)
+    //   ev_done[k] lane k's launch chain has finished (frames written); a
+    //              call whose frame buffer overlaps lane k's last one waits
+    //              for it before writing frames
+    hipEvent_t ev_in[kLanes] = {}, ev_read[kLanes] = {}, ev_done[kLanes] = {};
+    struct OutRange {
+        const char *lo = nullptr, *hi = nullptr;
+    } lane_out[kLanes];
+
+    // device copies of the decode chain's intermediate buffers
+    // (tpmd_set_tap), index [kind][stage + 1]
+    struct Tap {
+        void *dst = nullptr;
+        int64_t bytes = 0;
+    } taps[TPMD_TAP_KINDS][TPMD_MAX_STAGES + 1];
+    bool any_tap = false;
 
     // scratch for the per-stage entry points (grow-only)
     void *scr[4] = {};
@@ -291,6 +313,9 @@ struct tpmd_ctx {
             if (fs.copied[i]) (void) hipEventDestroy(fs.copied[i]);
         }
         if (fs.copy) (void) hipStreamDestroy(fs.copy);
+        for (int i = 0; i < kLanes; i++)
+            for (hipEvent_t e : {ev_in[i], ev_read[i], ev_done[i]})
+                if (e) (void) hipEventDestroy(e);
         if (own_stream) (void) hipStreamDestroy(own_stream);
         for (hipStream_t ls : lane_stream)
             if (ls) (void) hipStreamDestroy(ls);
@@ -496,6 +521,12 @@ bool drain_lanes(tpmd_ctx *c) {
     return true;
 }
 
+// every lane finished, lane 0's own stream included (before work moves to
+// another stream, which then uses lane 0's buffers)
+bool drain_all(tpmd_ctx *c) {
+    return drain_lanes(c) && c->hip_ok(hipStreamSynchronize(c->own_stream), "lane sync");
+}
+
 // stage entry points run on the caller's stream; NULL is HIP's null stream
 hipStream_t pick_stream(tpmd_ctx *, void *s) { return (hipStream_t) s; }
 
@@ -555,8 +586,12 @@ tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *st
                    hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) == hipSuccess;
     for (int i = 1; i < tpmd_ctx::kLanes && streams; i++)
         streams = hipStreamCreateWithFlags(&c->lane_stream[i], hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; i < tpmd_ctx::kLanes && streams; i++)
+        streams = hipEventCreateWithFlags(&c->ev_in[i], hipEventDisableTiming) == hipSuccess &&
+                  hipEventCreateWithFlags(&c->ev_read[i], hipEventDisableTiming) == hipSuccess &&
+                  hipEventCreateWithFlags(&c->ev_done[i], hipEventDisableTiming) == hipSuccess;
     if (!streams) {
-        fprintf(stderr, "tpmd_create: stream creation failed\n");
+        fprintf(stderr, "tpmd_create: stream or event creation failed\n");
         delete c;
         return nullptr;
     }
@@ -921,7 +956,47 @@ static ConvArgs conv_args(tpmd_ctx *c, const ConvW &cv, int n, int H, const void
     return a;
 }
 
-static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
+// bytes per frame of a tap (tpmd_set_tap), or -1 when the decode chain does
+// not hold that buffer
+static int64_t tap_frame_bytes(const tpmd_ctx *c, int kind, int stage) {
+    const int ns = c->ns;
+    if (stage < -1 || stage >= ns) return -1;
+    const int r = stage < 0 ? 4 : 8 << stage;
+    const int C = stage < 0 ? c->ic[0] : c->oc[stage];
+    const int64_t px = (int64_t) r * r;
+    switch (kind) {
+    case TPMD_TAP_TRUNK:
+        return stage < ns - 1 ? px * C * (int64_t) c->act_size() : -1;
+    case TPMD_TAP_C1:
+        return stage >= 0 ? px * C * (int64_t) c->act_size() : -1;
+    case TPMD_TAP_OUT:
+        return stage >= 0 && !fused_tail(c, C, r) ? px * C * 4 : -1;
+    case TPMD_TAP_FLOW:
+        return stage >= 0 ? px * 3 * 4 : -1;
+    case TPMD_TAP_RGB:
+        return stage >= 0 && stage < ns - 1 ? px * 3 * 4 : -1;
+    default:
+        return -1;
+    }
+}
+
+// copy frames [0, n) of a chain buffer to its registered tap, if any
+static bool tap_copy(tpmd_ctx *c, int kind, int stage, const void *src, int n, hipStream_t st) {
+    const tpmd_ctx::Tap &t = c->taps[kind][stage + 1];
+    if (!t.dst) return true;
+    const int64_t bytes = tap_frame_bytes(c, kind, stage) * n;
+    if (bytes > t.bytes) {
+        c->err = fmt("tap %d of stage %d holds %lld bytes, the decode needs %lld", kind, stage,
+                     (long long) t.bytes, (long long) bytes);
+        return false;
+    }
+    return c->hip_ok(hipMemcpyAsync(t.dst, src, (size_t) bytes, hipMemcpyDeviceToDevice, st), "tap copy");
+}
+
+// the whole batched decoder for frames [0, n) of the current lane on its
+// stream; the launch that writes img_dst (the last stage's tail) first waits
+// for `frames_after` when given
+static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst, hipEvent_t frames_after = nullptr) {
     hipStream_t st = c->stream;
     const bool f16 = c->f16;
     const int ns = c->ns, C0 = c->ic[0];
@@ -939,15 +1014,29 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
     if (!c->hip_ok(launch_modconv(conv_args(c, k1, n, 4, c->L->xs0, c->L->trunk, c->L->s_all + c->conv[1].s_off, f16), st),
                    "conv1"))
         return false;
+    if (c->any_tap && !tap_copy(c, TPMD_TAP_TRUNK, -1, c->L->trunk, n, st)) return false;
     for (int j = 0; j < ns; j++) {
         const int r = 8 << j, rh = r / 2, C = c->oc[j];
+        const bool last = j + 1 == ns;
         const ConvW &up = c->conv[1 + 2 * j], &dn = c->conv[2 + 2 * j];
         mark();
         if (!c->hip_ok(launch_modconv(conv_args(c, up, n, rh, c->L->trunk, c->L->c1, c->L->s_all + dn.s_off, f16), st),
                        "up-conv"))
             return false;
+        if (c->any_tap && !tap_copy(c, TPMD_TAP_C1, j, c->L->c1, n, st)) return false;
         mark();
-        const TailArgs ta = stage_tail_args(c, j, n, img_dst);
+        TailArgs ta = stage_tail_args(c, j, n, img_dst);
+        // the last stage keeps no flow map; a flow tap there is written by
+        // the tail itself
+        const tpmd_ctx::Tap &lf = c->taps[TPMD_TAP_FLOW][j + 1];
+        if (last && lf.dst) {
+            if (lf.bytes < tap_frame_bytes(c, TPMD_TAP_FLOW, j) * n) {
+                c->err = fmt("tap %d of stage %d is too small", TPMD_TAP_FLOW, j);
+                return false;
+            }
+            ta.flow_cur = (float *) lf.dst;
+        }
+        if (last && frames_after && !c->hip_ok(hipStreamWaitEvent(st, frames_after, 0), "wait")) return false;
         if (fused_tail(c, C, r)) {
             ConvArgs ca = conv_args(c, dn, n, r, c->L->c1, nullptr, nullptr, false);
             ca.tail = &ta;
@@ -957,24 +1046,32 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst) {
         } else {
             if (!c->hip_ok(launch_modconv(conv_args(c, dn, n, r, c->L->c1, c->L->outb, nullptr, false), st), "conv"))
                 return false;
+            if (c->any_tap && !tap_copy(c, TPMD_TAP_OUT, j, c->L->outb, n, st)) return false;
             mark();
             if (!c->hip_ok(launch_stage_tail(ta, f16, false, f16, st), "tail")) return false;
         }
+        if (c->any_tap && !last &&
+            (!tap_copy(c, TPMD_TAP_TRUNK, j, c->L->trunk, n, st) || !tap_copy(c, TPMD_TAP_FLOW, j, ta.flow_cur, n, st) ||
+             !tap_copy(c, TPMD_TAP_RGB, j, ta.rgb_cur, n, st)))
+            return false;
     }
     mark();
     return true;
 }
 
-static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device);
+static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device,
+                             int lane = -1);
 
 int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
     if (!check_ctx(c)) return -1;
     // device-resident decodes on the library's own stream rotate over the lanes;
     // every other form (host buffers, a caller's stream, per-stage
-    // profiling) runs on lane 0 after the other lanes have drained
-    const bool multi = on_device && imgs && !c->profile && c->stream == c->own_stream && tpmd_ctx::kLanes > 1;
+    // profiling, taps) runs on lane 0 after the other lanes have drained
+    const bool multi = on_device && imgs && !c->profile && !c->any_tap && c->stream == c->own_stream &&
+                       tpmd_ctx::kLanes > 1;
     if (!multi) {
         if (!drain_lanes(c)) return -1;
+        for (auto &o : c->lane_out) o = tpmd_ctx::OutRange{};
         return decode_batch_lane(c, styles, n, imgs, on_device);
     }
     const int k = c->next_lane;
@@ -982,13 +1079,15 @@ int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int 
     hipStream_t keep = c->stream;
     c->L = &c->lane[k];
     if (k > 0) c->stream = c->lane_stream[k];
-    const int rc = decode_batch_lane(c, styles, n, imgs, on_device);
+    const int rc = decode_batch_lane(c, styles, n, imgs, on_device, k);
     c->L = &c->lane[0];
     c->stream = keep;
     return rc;
 }
 
-static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
+// lane >= 0: a device-resident decode on that lane's stream, ordered against
+// the null stream for its latents and against the other lanes for its frames
+static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device, int lane) {
     if (!c->built) {
         c->err = "decoder not built";
         return -1;
@@ -1003,7 +1102,15 @@ static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *img
     }
     const size_t R = (size_t) c->out_res();
     const hipMemcpyKind k_in = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    // the latents are read after the caller's earlier null-stream work, and
+    // the null stream's later work waits for that read
+    if (lane >= 0 && !(c->hip_ok(hipEventRecord(c->ev_in[lane], nullptr), "event") &&
+                       c->hip_ok(hipStreamWaitEvent(c->stream, c->ev_in[lane], 0), "wait")))
+        return -1;
     if (!c->hip_ok(hipMemcpyAsync(c->L->lat, styles, (size_t) n * 512 * 4, k_in, c->stream), "style upload"))
+        return -1;
+    if (lane >= 0 && !(c->hip_ok(hipEventRecord(c->ev_read[lane], c->stream), "event") &&
+                       c->hip_ok(hipStreamWaitEvent(nullptr, c->ev_read[lane], 0), "wait")))
         return -1;
     if (c->profile) {
         const size_t need = (size_t) 2 + 3 * c->ns;
@@ -1014,7 +1121,23 @@ static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *img
         }
     }
     float *dst = (on_device && imgs) ? imgs : c->L->img;
-    if (!enqueue_decode(c, n, dst)) return -1;
+    // frames written into a buffer that another lane's in-flight call writes
+    // too land after that call's (a caller may reuse one frame buffer)
+    hipEvent_t after = nullptr;
+    const char *lo = (const char *) dst, *hi = lo + (size_t) n * 3 * R * R * 4;
+    if (lane >= 0) {
+        for (int l = 0; l < tpmd_ctx::kLanes; l++) {
+            const tpmd_ctx::OutRange &o = c->lane_out[l];
+            if (l == lane || !o.lo || hi <= o.lo || o.hi <= lo) continue;
+            if (after && !c->hip_ok(hipStreamWaitEvent(c->stream, after, 0), "wait")) return -1;
+            after = c->ev_done[l];
+        }
+    }
+    if (!enqueue_decode(c, n, dst, after)) return -1;
+    if (lane >= 0) {
+        if (!c->hip_ok(hipEventRecord(c->ev_done[lane], c->stream), "event")) return -1;
+        c->lane_out[lane] = {lo, hi};
+    }
     if (!on_device) {
         if (imgs && !c->hip_ok(hipMemcpyAsync(imgs, c->L->img, (size_t) n * 3 * R * R * 4, hipMemcpyDeviceToHost,
                                               c->stream), "image download"))
@@ -1149,6 +1272,7 @@ int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, i
     // leave every stream idle: the slots may be reused by the next call
     const bool drained = c->hip_ok(hipStreamSynchronize(f.copy), "drain") && drain_lanes(c) &&
                          c->hip_ok(hipStreamSynchronize(c->stream), "drain");
+    for (auto &o : c->lane_out) o = tpmd_ctx::OutRange{};
     c->profile = prof;
     return ok && drained ? n_frames : -1;
 }
@@ -1159,14 +1283,18 @@ int tpmd_decode(tpmd_ctx *c, const float *style, float *img) {
 
 int tpmd_set_stream(tpmd_ctx *c, void *stream) {
     if (!check_ctx(c)) return -1;
-    if (!drain_lanes(c)) return -1;
+    // lane 0's buffers move to the new stream: nothing may still use them on
+    // the library's streams or on the previous caller stream
+    if (!drain_all(c)) return -1;
+    if (c->stream != c->own_stream && !c->hip_ok(hipStreamSynchronize(c->stream), "stream sync")) return -1;
+    for (auto &o : c->lane_out) o = tpmd_ctx::OutRange{};
     c->stream = (hipStream_t) stream;
     return 0;
 }
 
 int tpmd_sync(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
-    return drain_lanes(c) && c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
+    return drain_all(c) && c->hip_ok(hipStreamSynchronize(c->stream), "sync") ? 0 : -1;
 }
 
 int tpmd_profile_stages(tpmd_ctx *c, int enable) {
@@ -1180,6 +1308,34 @@ int tpmd_stage_times(const tpmd_ctx *c, float *us, int max_slots) {
     const int n = (int) c->times.size() < max_slots ? (int) c->times.size() : max_slots;
     for (int i = 0; i < n; i++) us[i] = c->times[(size_t) i];
     return n;
+}
+
+int64_t tpmd_tap_frame_bytes(const tpmd_ctx *c, int kind, int stage) {
+    return c ? tap_frame_bytes(c, kind, stage) : -1;
+}
+
+int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
+    if (!check_ctx(c)) return -1;
+    if (kind < 0 || kind >= TPMD_TAP_KINDS || stage < -1 || stage >= c->ns) {
+        c->err = "tpmd_set_tap: bad kind or stage";
+        return -1;
+    }
+    if (dst && tap_frame_bytes(c, kind, stage) < 0) {
+        c->err = fmt("tpmd_set_tap: the decode chain holds no buffer of kind %d at stage %d", kind, stage);
+        return -1;
+    }
+    if (dst && bytes < 0) {
+        c->err = "tpmd_set_tap: negative size";
+        return -1;
+    }
+    // a call with taps runs on lane 0 after the other lanes drain: none of
+    // them may still write a tap buffer being replaced
+    if (!drain_lanes(c)) return -1;
+    c->taps[kind][stage + 1] = {dst, dst ? bytes : 0};
+    c->any_tap = false;
+    for (const auto &row : c->taps)
+        for (const auto &t : row) c->any_tap = c->any_tap || t.dst;
+    return 0;
 }
 
 int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,

@@ -29,6 +29,7 @@ HEADER = os.path.join(os.path.dirname(_HERE), "include", "tpmd.h")
 
 W_F16_FILE = 1
 W_FOLDED = 2
+TAP_TRUNK, TAP_C1, TAP_OUT, TAP_FLOW, TAP_RGB = range(5)
 FRAME_F32 = 0
 FRAME_RGB24 = 1
 FRAME_CB = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p)
@@ -71,6 +72,8 @@ def lib():
             "tpmd_set_stream": (I, [P, P]),
             "tpmd_profile_stages": (I, [P, I]),
             "tpmd_stage_times": (I, [P, P, I]),
+            "tpmd_set_tap": (I, [P, I, I, P, I64]),
+            "tpmd_tap_frame_bytes": (I64, [P, I, I]),
             "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
             "tpmd_stage_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P]),
             "tpmd_stage_conv_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P, P]),
@@ -236,9 +239,28 @@ class MotionDecoder:
         return out
 
     def decode_batch_device(self, styles_dev, imgs_dev):
-        """device (n, 512) -> device (n, 3, R, R), enqueued on the decoder stream"""
+        """device (n, 512) float32 -> device (n, 3, R, R) float32, asynchronous
+        (tpmd_decode_batch's on-device ordering rules; frames complete after
+        sync())"""
+        import torch
+        for t, what in ((styles_dev, "styles"), (imgs_dev, "imgs")):
+            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32):
+                raise TpmdError(f"decode_batch_device: {what} must be a float32 CUDA tensor")
+        if styles_dev.dim() != 2 or styles_dev.shape[1] != 512:
+            raise TpmdError("decode_batch_device: styles must be (n, 512)")
         n = styles_dev.shape[0]
+        if imgs_dev.numel() < n * 3 * self.res * self.res:
+            raise TpmdError(f"decode_batch_device: imgs must hold ({n}, 3, {self.res}, {self.res})")
         self._check(lib().tpmd_decode_batch(self.h, _ptr(styles_dev), n, _ptr(imgs_dev), 1))
+
+    def tap_frame_bytes(self, kind, stage):
+        return lib().tpmd_tap_frame_bytes(self.h, kind, stage)
+
+    def set_tap(self, kind, stage, buf):
+        """copy the decode chain's buffer `kind` of `stage` into the CUDA
+        tensor buf on every later decode_batch (None removes the tap)"""
+        nb = buf.numel() * buf.element_size() if buf is not None else 0
+        self._check(lib().tpmd_set_tap(self.h, kind, stage, _ptr(buf), nb))
 
     def decode_frames(self, styles, fmt=FRAME_F32, to_buffer=True, cb=None, out=None):
         """a clip of latents (n, 512) through tpmd_decode_frames: returns the

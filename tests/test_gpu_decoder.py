@@ -113,3 +113,47 @@ def test_error_contract(torch_cuda):
     assert tpmd.MotionDecoder.__init__  # constructor rejects bad configs:
     with pytest.raises(tpmd.TpmdError):
         tpmd.MotionDecoder("f32", 2, (64, 48), (48, 64))
+
+
+def test_lanes_read_latents_in_order(om, torch_cuda):
+    """one latent buffer refilled on torch's default stream (HIP's null
+    stream) right after each device decode, with no synchronisation: every
+    call decodes the latents it was given (a call reads them after earlier
+    null-stream work, and later null-stream work waits for that read)"""
+    torch = torch_cuda
+    assert torch.cuda.current_stream().cuda_stream == 0, "torch's current stream is not the null stream"
+    _, dec, lat = _decoders(om, "f16", SMALL_IC, SMALL_OC, 8, 2)
+    starts = range(0, 8, 2)
+    want = [dec.decode_batch(lat[t:t + 2]) for t in starts]
+    src = torch.from_numpy(lat).cuda()
+    sd = torch.empty((2, 512), device="cuda")
+    outs = [torch.empty((2, 3, 512, 512), device="cuda") for _ in starts]
+    torch.cuda.synchronize()
+    for o, t in zip(outs, starts):
+        sd.copy_(src[t:t + 2])
+        dec.decode_batch_device(sd, o)
+    dec.sync()
+    for o, w in zip(outs, want):
+        assert np.array_equal(o.cpu().numpy(), w)
+
+
+def test_lanes_reuse_one_frame_buffer(om, torch_cuda):
+    """four device decodes into one frame buffer (every lane, then lane 0
+    again, the calls overlapping on the GPU): after tpmd_sync it holds the
+    last call's frames; a buffer that only partly overlaps the previous
+    call's is ordered too"""
+    torch = torch_cuda
+    _, dec, lat = _decoders(om, "f16", SMALL_IC, SMALL_OC, 8, 2)
+    want = dec.decode_batch(lat[6:8])
+    src = torch.from_numpy(lat).cuda()
+    out = torch.empty((3, 3, 512, 512), device="cuda")
+    torch.cuda.synchronize()
+    for t in range(0, 8, 2):
+        dec.decode_batch_device(src[t:t + 2], out[:2])
+    dec.sync()
+    assert np.array_equal(out[:2].cpu().numpy(), want)
+    # frames 1..2 of the buffer after frames 0..1: the shared frame holds the later call's
+    dec.decode_batch_device(src[0:2], out[0:2])
+    dec.decode_batch_device(src[6:8], out[1:3])
+    dec.sync()
+    assert np.array_equal(out[1:3].cpu().numpy(), want)
