@@ -29,7 +29,7 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", 
 
 SOURCES = ["k_gather.hip", "k_conv.hip", "k_conv_async.hip", "k_conv_fused.hip", "k_conv_up.hip", "k_conv_halo.hip", "k_tail.hip", "k_style.hip", "k_enc.hip", "k_fmt.hip", "tpmd.cpp", "tpme.cpp", "tpfm.cpp"]
 # plain C++ over the C ABI (no HIP): the tp::motion_dec shim, in the library
-HOST_SOURCES = ["motion_dec.cpp", "motion_enc.cpp", "gguf.cpp"]
+HOST_SOURCES = ["motion_dec.cpp", "motion_enc.cpp", "gguf.cpp", "gguf_abi.cpp"]
 CXX = os.environ.get("CXX", "g++")
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOSTDIR}"]
 SHIM_CHECK = os.path.join(PKG, "shim_check")

@@ -13,6 +13,7 @@
 #include <string>
 #include <vector>
 
+#include "tpmd_guard.h"
 #include "tpmd.h"
 #include "tpmd_fmt.h"
 
@@ -329,7 +330,7 @@ void tpfm_default_config(tpfm_config *g) {
     g->r_cfg = 1.0f;
 }
 
-tpfm_ctx *tpfm_create(int device, const char *ftype, const tpfm_config *cfg) {
+static tpfm_ctx *tpfm_create_body(int device, const char *ftype, const tpfm_config *cfg) {
     if (!ftype || (strcmp(ftype, "f32") != 0 && strcmp(ftype, "f16") != 0) || !cfg) {
         fprintf(stderr, "tpfm_create: ftype must be f32 or f16, and a config is needed\n");
         return nullptr;
@@ -380,7 +381,7 @@ const char *tpfm_weight_name(const tpfm_ctx *c, int i, int64_t *n, int *is_matri
     return t.first.c_str();
 }
 
-int tpfm_set_weight(tpfm_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+static int tpfm_set_weight_body(tpfm_ctx *c, const char *name, const float *data, int64_t n, int flags) {
     if (!check(c)) return -1;
     if (!name || !data || n <= 0) {
         c->err = "tpfm_set_weight: null name/data or empty tensor";
@@ -407,7 +408,7 @@ int tpfm_set_weight(tpfm_ctx *c, const char *name, const float *data, int64_t n,
     return 0;
 }
 
-int tpfm_prepare(tpfm_ctx *c) {
+static int tpfm_prepare_body(tpfm_ctx *c) {
     if (!check(c)) return -1;
     c->free_all();
     c->prepared = false;
@@ -493,7 +494,7 @@ int tpfm_prepare(tpfm_ctx *c) {
     return 0;
 }
 
-int tpfm_forward(tpfm_ctx *c, const float *x60, const float *cond, float t, float *v_out) {
+static int tpfm_forward_body(tpfm_ctx *c, const float *x60, const float *cond, float t, float *v_out) {
     if (!check(c)) return -1;
     if (!c->prepared) {
         c->err = "FMT not prepared";
@@ -516,7 +517,7 @@ int tpfm_forward(tpfm_ctx *c, const float *x60, const float *cond, float t, floa
     return 0;
 }
 
-int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const float *prev_wa,
+static int tpfm_sample_chunk_body(tpfm_ctx *c, const float *wr, const float *prev_x, const float *prev_wa,
                       const float *cond_audio, int emotion, const float *x0, float *motion_out) {
     if (!check(c)) return -1;
     if (!c->prepared) {
@@ -564,6 +565,30 @@ int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const f
         !c->hip_ok(hipStreamSynchronize(st), "sample sync"))
         return -1;
     return 0;
+}
+
+
+// ---- entry points that allocate host memory, exception-safe
+
+tpfm_ctx *tpfm_create(int device, const char *ftype, const tpfm_config *cfg) {
+    return guarded((void *) nullptr, [&] { return tpfm_create_body(device, ftype, cfg); });
+}
+
+int tpfm_set_weight(tpfm_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+    return guarded(c, [&] { return tpfm_set_weight_body(c, name, data, n, flags); });
+}
+
+int tpfm_prepare(tpfm_ctx *c) {
+    return guarded(c, [&] { return tpfm_prepare_body(c); });
+}
+
+int tpfm_forward(tpfm_ctx *c, const float *x60, const float *cond, float t, float *v_out) {
+    return guarded(c, [&] { return tpfm_forward_body(c, x60, cond, t, v_out); });
+}
+
+int tpfm_sample_chunk(tpfm_ctx *c, const float *wr, const float *prev_x, const float *prev_wa,
+                      const float *cond_audio, int emotion, const float *x0, float *motion_out) {
+    return guarded(c, [&] { return tpfm_sample_chunk_body(c, wr, prev_x, prev_wa, cond_audio, emotion, x0, motion_out); });
 }
 
 }  // extern "C"

@@ -8,6 +8,7 @@
 // enqueues the whole batched decoder on one HIP stream:
 //   style GEMV, demod, conv1 input, conv1,
 //   then per stage j: sub-pixel up-conv, dense conv, fused tail.
+#include "tpmd_guard.h"
 #include "tpmd.h"
 
 #include <hip/hip_runtime.h>
@@ -537,7 +538,7 @@ extern "C" {
 
 int tpmd_abi_version(void) { return TPMD_ABI_VERSION; }
 
-tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *stage_ic,
+static tpmd_ctx *tpmd_create_body(int device, const char *ftype, int n_stages, const int *stage_ic,
                       const int *stage_oc) {
     const std::string ft = ftype ? ftype : "f32";
     if (ft != "f32" && ft != "f16") {
@@ -603,7 +604,7 @@ void tpmd_destroy(tpmd_ctx *c) { delete c; }
 
 const char *tpmd_last_error(const tpmd_ctx *c) { return c ? c->err.c_str() : "no context"; }
 
-int tpmd_set_weight(tpmd_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+static int tpmd_set_weight_body(tpmd_ctx *c, const char *name, const float *data, int64_t n, int flags) {
     if (!check_ctx(c)) return -1;
     if (!name || !data || n <= 0) {
         c->err = "tpmd_set_weight: null name/data or empty tensor";
@@ -650,7 +651,7 @@ const char *tpmd_weight_name(const tpmd_ctx *c, int i, int64_t *n, int *is_matri
     return t.first.c_str();
 }
 
-int tpmd_prepare(tpmd_ctx *c) {
+static int tpmd_prepare_body(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
     if (!drain_lanes(c)) return -1;
     for (void *p : c->allocs) (void) hipFree(p);
@@ -758,7 +759,7 @@ int tpmd_prepare(tpmd_ctx *c) {
     return 0;
 }
 
-int tpmd_build(tpmd_ctx *c, int max_batch) {
+static int tpmd_build_body(tpmd_ctx *c, int max_batch) {
     if (!check_ctx(c)) return -1;
     if (!drain_lanes(c)) return -1;
     if (!c->prepared) {
@@ -1062,7 +1063,7 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst, hipEvent_t frames
 static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device,
                              int lane = -1);
 
-int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
+static int tpmd_decode_batch_body(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
     if (!check_ctx(c)) return -1;
     // device-resident decodes on the library's own stream rotate over the lanes;
     // every other form (host buffers, a caller's stream, per-stage
@@ -1191,7 +1192,7 @@ static bool frame_slots(tpmd_ctx *c, size_t bytes) {
     return true;
 }
 
-int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, int format, void *out,
+static int64_t tpmd_decode_frames_body(tpmd_ctx *c, const float *styles, int64_t n_frames, int format, void *out,
                            tpmd_frame_cb cb, void *ud) {
     if (!check_ctx(c)) return -1;
     if (!drain_lanes(c)) return -1;
@@ -1314,7 +1315,7 @@ int64_t tpmd_tap_frame_bytes(const tpmd_ctx *c, int kind, int stage) {
     return c ? tap_frame_bytes(c, kind, stage) : -1;
 }
 
-int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
+static int tpmd_set_tap_body(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
     if (!check_ctx(c)) return -1;
     if (kind < 0 || kind >= TPMD_TAP_KINDS || stage < -1 || stage >= c->ns) {
         c->err = "tpmd_set_tap: bad kind or stage";
@@ -1338,7 +1339,7 @@ int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
     return 0;
 }
 
-int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
+static int tpmd_modconv_body(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
                  void *stream) {
     if (!check_ctx(c)) return -1;
     if (!c->prepared) {
@@ -1390,7 +1391,7 @@ int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, con
     return 0;
 }
 
-int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
+static int tpmd_stage_tail_body(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
                     const float *rgb_prev, float *flow, float *trunk, float *rgb, float *warp,
                     void *stream) {
     if (!check_ctx(c)) return -1;
@@ -1433,7 +1434,7 @@ int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_
     return c->hip_ok(launch_stage_tail(a, c->f16, false, false, pick_stream(c, stream)), "tail") ? 0 : -1;
 }
 
-int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float *s_conv, const float *s_flow,
+static int tpmd_stage_conv_tail_body(tpmd_ctx *c, int j, const float *c1, int n, const float *s_conv, const float *s_flow,
                          const float *flow_prev, const float *rgb_prev, float *flow, float *trunk, float *rgb,
                          float *warp, void *stream) {
     if (!check_ctx(c)) return -1;
@@ -1554,6 +1555,56 @@ int tpmd_upfirdn2x(const float *x, const float *k4, float *y, int W, int H, int6
 int tpmd_flow_grid(const float *fl, const float *xs, float *y, int64_t N, void *stream) {
     if (!fl || !xs || !y || N < 0) return -1;
     return launch_flow_grid(fl, xs, y, N, (hipStream_t) stream) == hipSuccess ? 0 : -1;
+}
+
+
+// ---- entry points that allocate host memory, exception-safe
+
+tpmd_ctx *tpmd_create(int device, const char *ftype, int n_stages, const int *stage_ic,
+                      const int *stage_oc) {
+    return guarded((void *) nullptr, [&] { return tpmd_create_body(device, ftype, n_stages, stage_ic, stage_oc); });
+}
+
+int tpmd_set_weight(tpmd_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+    return guarded(c, [&] { return tpmd_set_weight_body(c, name, data, n, flags); });
+}
+
+int tpmd_prepare(tpmd_ctx *c) {
+    return guarded(c, [&] { return tpmd_prepare_body(c); });
+}
+
+int tpmd_build(tpmd_ctx *c, int max_batch) {
+    return guarded(c, [&] { return tpmd_build_body(c, max_batch); });
+}
+
+int tpmd_decode_batch(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device) {
+    return guarded(c, [&] { return tpmd_decode_batch_body(c, styles, n, imgs, on_device); });
+}
+
+int64_t tpmd_decode_frames(tpmd_ctx *c, const float *styles, int64_t n_frames, int format, void *out,
+                           tpmd_frame_cb cb, void *ud) {
+    return guarded(c, [&] { return tpmd_decode_frames_body(c, styles, n_frames, format, out, cb, ud); });
+}
+
+int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
+    return guarded(c, [&] { return tpmd_set_tap_body(c, kind, stage, dst, bytes); });
+}
+
+int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
+                 void *stream) {
+    return guarded(c, [&] { return tpmd_modconv_body(c, conv, x, n, H, W, s, y, stream); });
+}
+
+int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
+                    const float *rgb_prev, float *flow, float *trunk, float *rgb, float *warp,
+                    void *stream) {
+    return guarded(c, [&] { return tpmd_stage_tail_body(c, j, out, n, s_flow, flow_prev, rgb_prev, flow, trunk, rgb, warp, stream); });
+}
+
+int tpmd_stage_conv_tail(tpmd_ctx *c, int j, const float *c1, int n, const float *s_conv, const float *s_flow,
+                         const float *flow_prev, const float *rgb_prev, float *flow, float *trunk, float *rgb,
+                         float *warp, void *stream) {
+    return guarded(c, [&] { return tpmd_stage_conv_tail_body(c, j, c1, n, s_conv, s_flow, flow_prev, rgb_prev, flow, trunk, rgb, warp, stream); });
 }
 
 }  // extern "C"

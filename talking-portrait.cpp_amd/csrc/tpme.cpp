@@ -13,6 +13,7 @@
 #include <string>
 #include <vector>
 
+#include "tpmd_guard.h"
 #include "tpmd.h"
 #include "tpmd_enc.h"
 
@@ -223,7 +224,7 @@ float *upload_value(tpme_ctx *c, const std::string &name, bool *is16 = nullptr) 
 
 extern "C" {
 
-tpme_ctx *tpme_create(int device, const char *ftype, int n_blocks, const int *ch_in, const int *ch_out) {
+static tpme_ctx *tpme_create_body(int device, const char *ftype, int n_blocks, const int *ch_in, const int *ch_out) {
     static const int REF_IN[7] = {32, 64, 128, 256, 512, 512, 512};
     static const int REF_OUT[7] = {64, 128, 256, 512, 512, 512, 512};
     if (!ftype || (strcmp(ftype, "f32") != 0 && strcmp(ftype, "f16") != 0)) {
@@ -275,7 +276,7 @@ const char *tpme_weight_name(const tpme_ctx *c, int i, int64_t *n, int *is_matri
     return t.first.c_str();
 }
 
-int tpme_set_weight(tpme_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+static int tpme_set_weight_body(tpme_ctx *c, const char *name, const float *data, int64_t n, int flags) {
     if (!check(c)) return -1;
     if (!name || !data || n <= 0) {
         c->err = "tpme_set_weight: null name/data or empty tensor";
@@ -312,7 +313,7 @@ int tpme_set_weight(tpme_ctx *c, const char *name, const float *data, int64_t n,
     return 0;
 }
 
-int tpme_prepare(tpme_ctx *c) {
+static int tpme_prepare_body(tpme_ctx *c) {
     if (!check(c)) return -1;
     c->free_all();
     c->prepared = c->ran = false;
@@ -385,7 +386,7 @@ int tpme_prepare(tpme_ctx *c) {
     return 0;
 }
 
-int tpme_run(tpme_ctx *c, const float *image, int on_device) {
+static int tpme_run_body(tpme_ctx *c, const float *image, int on_device) {
     if (!check(c)) return -1;
     if (!c->prepared) {
         c->err = "encoder not prepared";
@@ -504,7 +505,7 @@ const float *tpme_feat(const tpme_ctx *c, int j, int *C, int *r) {
     return c->lvl[l];
 }
 
-int64_t tpme_level(tpme_ctx *c, int level, float *dst) {
+static int64_t tpme_level_body(tpme_ctx *c, int level, float *dst) {
     if (!check(c)) return -1;
     if (level < 0 || level > c->nb) {
         c->err = "tpme_level: bad level";
@@ -518,6 +519,29 @@ int64_t tpme_level(tpme_ctx *c, int level, float *dst) {
     }
     if (!c->hip_ok(hipMemcpy(dst, c->lvl[level], (size_t) n * 4, hipMemcpyDeviceToHost), "copy")) return -1;
     return n;
+}
+
+
+// ---- entry points that allocate host memory, exception-safe
+
+tpme_ctx *tpme_create(int device, const char *ftype, int n_blocks, const int *ch_in, const int *ch_out) {
+    return guarded((void *) nullptr, [&] { return tpme_create_body(device, ftype, n_blocks, ch_in, ch_out); });
+}
+
+int tpme_set_weight(tpme_ctx *c, const char *name, const float *data, int64_t n, int flags) {
+    return guarded(c, [&] { return tpme_set_weight_body(c, name, data, n, flags); });
+}
+
+int tpme_prepare(tpme_ctx *c) {
+    return guarded(c, [&] { return tpme_prepare_body(c); });
+}
+
+int tpme_run(tpme_ctx *c, const float *image, int on_device) {
+    return guarded(c, [&] { return tpme_run_body(c, image, on_device); });
+}
+
+int64_t tpme_level(tpme_ctx *c, int level, float *dst) {
+    return guarded(c, [&] { return tpme_level_body(c, level, dst); });
 }
 
 }  // extern "C"

@@ -1,59 +1,131 @@
-// GGUF v3 reader (see gguf.h) and the C entry points tpmd_load_gguf /
-// tpme_load_gguf / tpfm_read_config / tpfm_load_gguf / tpmd_gguf_read_tensor
-// of include/tpmd.h.
+// GGUF v3 reader (see gguf.h).  Plain C++ with no device code: the library
+// links it, and host/Makefile.sanitize builds it with AddressSanitizer and
+// UndefinedBehaviorSanitizer under the gguf_check driver.
 #include "gguf.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <cstdio>
 #include <cstring>
-
-#include "tpmd.h"
 
 namespace tp {
 
 namespace {
 
-struct cursor {
-    const uint8_t *p, *end;
-    bool ok = true;
-    template <typename T>
-    T get() {
-        T v{};
-        if ((size_t) (end - p) < sizeof(T)) {
-            ok = false;
-            return v;
-        }
-        memcpy(&v, p, sizeof(T));
-        p += sizeof(T);
-        return v;
-    }
-    std::string str() {
-        const uint64_t n = get<uint64_t>();
-        if (!ok || n > (uint64_t) (end - p) || n > (1u << 20)) {
-            ok = false;
-            return {};
-        }
-        std::string s((const char *) p, (size_t) n);
-        p += n;
-        return s;
-    }
+// metadata value types of the format
+enum : uint32_t {
+    GT_U8 = 0, GT_I8, GT_U16, GT_I16, GT_U32, GT_I32, GT_F32, GT_BOOL, GT_STRING, GT_ARRAY,
+    GT_U64, GT_I64, GT_F64,
 };
 
-bool read_all(const std::string &path, std::vector<uint8_t> &out, std::string &err) {
-    FILE *f = fopen(path.c_str(), "rb");
-    if (!f) {
-        err = path + ": cannot open";
-        return false;
+// bytes of a fixed-size value type; 0 for string and array, -1 unknown
+int fixed_bytes(uint32_t t) {
+    switch (t) {
+        case GT_U8: case GT_I8: case GT_BOOL: return 1;
+        case GT_U16: case GT_I16: return 2;
+        case GT_U32: case GT_I32: case GT_F32: return 4;
+        case GT_U64: case GT_I64: case GT_F64: return 8;
+        case GT_STRING: case GT_ARRAY: return 0;
+        default: return -1;
     }
-    bool ok = fseek(f, 0, SEEK_END) == 0;
-    const long sz = ok ? ftell(f) : -1;
-    ok = ok && sz >= 0 && fseek(f, 0, SEEK_SET) == 0;
-    if (ok) {
-        out.resize((size_t) sz);
-        ok = fread(out.data(), 1, out.size(), f) == out.size();
+}
+
+template <typename T>
+T load_le(const uint8_t *p) {
+    T v;
+    memcpy(&v, p, sizeof v);  // the format and the host are little-endian
+    return v;
+}
+
+// a fixed-size scalar as a double (bool as 0 / 1)
+double number_of(uint32_t t, const uint8_t *p) {
+    switch (t) {
+        case GT_U8: return p[0];
+        case GT_I8: return (int8_t) p[0];
+        case GT_BOOL: return p[0] ? 1.0 : 0.0;
+        case GT_U16: return load_le<uint16_t>(p);
+        case GT_I16: return load_le<int16_t>(p);
+        case GT_U32: return load_le<uint32_t>(p);
+        case GT_I32: return load_le<int32_t>(p);
+        case GT_F32: return load_le<float>(p);
+        case GT_U64: return (double) load_le<uint64_t>(p);
+        case GT_I64: return (double) load_le<int64_t>(p);
+        default: return load_le<double>(p);
     }
-    fclose(f);
-    if (!ok) err = path + ": read error";
-    return ok;
+}
+
+// bounds-checked sequential reads over the mapped file; a read that would
+// run past the end fails and the parse stops there
+class span_reader {
+  public:
+    span_reader(const uint8_t *b, uint64_t n) : b_(b), n_(n) {}
+    uint64_t pos() const { return pos_; }
+    bool take(uint64_t len, const uint8_t *&p) {
+        if (len > n_ - pos_) return false;
+        p = b_ + pos_;
+        pos_ += len;
+        return true;
+    }
+    template <typename T>
+    bool scalar(T &v) {
+        const uint8_t *p;
+        if (!take(sizeof(T), p)) return false;
+        v = load_le<T>(p);
+        return true;
+    }
+    bool text(std::string &s) {
+        uint64_t len;
+        const uint8_t *p;
+        if (!scalar(len) || !take(len, p)) return false;
+        s.assign((const char *) p, (size_t) len);
+        return true;
+    }
+
+  private:
+    const uint8_t *b_;
+    uint64_t n_, pos_ = 0;
+};
+
+enum class walk { ok, truncated, bad_type };
+
+// one metadata value of type t: scalars into *num, strings into *str,
+// arrays (of any element type, nested up to 4 deep) walked and dropped
+walk walk_value(span_reader &r, uint32_t t, int depth, double *num, std::string *str) {
+    const int fb = fixed_bytes(t);
+    if (fb < 0) return walk::bad_type;
+    if (fb > 0) {
+        const uint8_t *p;
+        if (!r.take((uint64_t) fb, p)) return walk::truncated;
+        if (num) *num = number_of(t, p);
+        return walk::ok;
+    }
+    if (t == GT_STRING) {
+        std::string s;
+        if (!r.text(s)) return walk::truncated;
+        if (str) *str = std::move(s);
+        return walk::ok;
+    }
+    uint32_t et;
+    uint64_t count;
+    if (!r.scalar(et) || !r.scalar(count)) return walk::truncated;
+    const int efb = fixed_bytes(et);
+    if (efb < 0 || (et == GT_ARRAY && depth >= 4)) return walk::bad_type;
+    if (efb > 0) {
+        uint64_t bytes;
+        const uint8_t *p;
+        if (__builtin_mul_overflow(count, (uint64_t) efb, &bytes) || !r.take(bytes, p)) return walk::truncated;
+        return walk::ok;
+    }
+    // strings / arrays: each element takes at least 8 bytes, so a count
+    // beyond the file ends at the first truncated element
+    for (uint64_t i = 0; i < count; i++) {
+        const walk w = walk_value(r, et, depth + 1, nullptr, nullptr);
+        if (w != walk::ok) return w;
+    }
+    return walk::ok;
 }
 
 }  // namespace
@@ -84,101 +156,112 @@ float half_to_float(uint16_t h) {
     return f;
 }
 
+void gguf_file::unmap() {
+    if (base_ && size_) munmap((void *) base_, (size_t) size_);
+    base_ = nullptr;
+    size_ = 0;
+}
+
 bool gguf_file::open(const std::string &path, const char *expect_arch, std::string &err) {
+    unmap();
     path_ = path;
     kv_num.clear();
     kv_str.clear();
     tensors.clear();
-    index.clear();
-    if (!read_all(path, data_, err)) return false;
-    cursor c{data_.data(), data_.data() + data_.size()};
-    char magic[4];
-    for (char &ch : magic) ch = (char) c.get<uint8_t>();
-    if (!c.ok || memcmp(magic, "GGUF", 4) != 0) {
-        err = path + ": not a GGUF file";
+    index_.clear();
+    auto bad = [&](const std::string &what) {
+        err = path + ": " + what;
         return false;
+    };
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return bad("cannot open");
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 0) {
+        ::close(fd);
+        return bad("cannot stat");
     }
-    if (c.get<uint32_t>() != 3) {
-        err = path + ": unsupported GGUF version";
-        return false;
-    }
-    const uint64_t n_tensors = c.get<uint64_t>(), n_kv = c.get<uint64_t>();
-    if (!c.ok || n_tensors > 100000 || n_kv > 100000) {
-        err = path + ": corrupt header";
-        return false;
-    }
-    for (uint64_t i = 0; i < n_kv && c.ok; i++) {
-        const std::string key = c.str();
-        const uint32_t vt = c.get<uint32_t>();
-        switch (vt) {
-            case 4: kv_num[key] = c.get<uint32_t>(); break;
-            case 5: kv_num[key] = c.get<int32_t>(); break;
-            case 6: kv_num[key] = c.get<float>(); break;
-            case 7: kv_num[key] = c.get<uint8_t>() ? 1 : 0; break;
-            case 8: kv_str[key] = c.str(); break;
-            default:
-                err = path + ": unsupported KV type " + std::to_string(vt) + " for " + key;
-                return false;
+    size_ = (uint64_t) st.st_size;
+    if (size_ > 0) {
+        void *m = mmap(nullptr, (size_t) size_, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) {
+            ::close(fd);
+            size_ = 0;
+            return bad("cannot map");
         }
+        base_ = (const uint8_t *) m;
     }
-    if (!c.ok) {
-        err = path + ": truncated KV section";
-        return false;
+    ::close(fd);
+
+    span_reader r(base_, size_);
+    const uint8_t *magic;
+    if (!r.take(4, magic) || memcmp(magic, "GGUF", 4) != 0) return bad("not a GGUF file");
+    uint32_t version;
+    if (!r.scalar(version) || version != 3) return bad("unsupported GGUF version");
+    uint64_t n_tensors, n_kv;
+    // a metadata pair takes at least 12 bytes and a tensor record 24
+    if (!r.scalar(n_tensors) || !r.scalar(n_kv) || n_kv > size_ / 12 || n_tensors > size_ / 24)
+        return bad("corrupt header");
+
+    for (uint64_t i = 0; i < n_kv; i++) {
+        std::string key;
+        uint32_t vt;
+        if (!r.text(key) || !r.scalar(vt)) return bad("truncated KV section");
+        double num = 0;
+        std::string str;
+        const bool scalar = fixed_bytes(vt) > 0;
+        const walk w = walk_value(r, vt, 0, scalar ? &num : nullptr, vt == GT_STRING ? &str : nullptr);
+        if (w == walk::truncated) return bad("truncated KV section");
+        if (w == walk::bad_type) return bad("unsupported KV type " + std::to_string(vt) + " for " + key);
+        if (scalar) kv_num[key] = num;
+        if (vt == GT_STRING) kv_str[key] = std::move(str);
     }
     if (expect_arch) {
         auto it = kv_str.find("general.architecture");
-        if (it == kv_str.end() || it->second != expect_arch) {
-            err = path + ": unexpected architecture '" + (it == kv_str.end() ? "<none>" : it->second) +
-                  "', want " + expect_arch;
-            return false;
-        }
-    }
-    tensors.resize((size_t) n_tensors);
-    for (auto &t : tensors) {
-        t.name = c.str();
-        const uint32_t nd = c.get<uint32_t>();
-        if (!c.ok || nd > 8) {
-            err = path + ": corrupt tensor info";
-            return false;
-        }
-        for (uint32_t j = 0; j < nd; j++) {
-            const uint64_t d = c.get<uint64_t>();
-            if (d > (1ull << 40)) c.ok = false;
-            t.dims.push_back(d);
-            t.n *= (int64_t) (d ? d : 1);
-        }
-        t.type = c.get<uint32_t>();
-        t.offset = c.get<uint64_t>();
-        if (c.ok && t.type > 1) {
-            err = path + ": tensor " + t.name + " has unsupported type";
-            return false;
-        }
-        if (!c.ok) break;
-    }
-    if (!c.ok) {
-        err = path + ": truncated tensor info section";
-        return false;
+        if (it == kv_str.end() || it->second != expect_arch)
+            return bad("unexpected architecture '" + (it == kv_str.end() ? std::string("<none>") : it->second) +
+                       "', want " + expect_arch);
     }
     uint64_t align = 32;
-    auto al = kv_num.find("general.alignment");
-    if (al != kv_num.end() && al->second >= 1 && al->second <= 4096) align = (uint64_t) al->second;
-    const size_t pre = (size_t) (c.p - data_.data());
-    data_off_ = (size_t) ((pre + align - 1) / align * align);
+    if (auto al = kv_num.find("general.alignment"); al != kv_num.end()) {
+        const double a = al->second;
+        if (!(a >= 1 && a <= 65536) || a != (double) (uint64_t) a || ((uint64_t) a & ((uint64_t) a - 1)))
+            return bad("corrupt header (general.alignment)");
+        align = (uint64_t) a;
+    }
+
+    tensors.resize((size_t) n_tensors);
     for (size_t i = 0; i < tensors.size(); i++) {
-        const tensor &t = tensors[i];
-        const size_t esz = t.type == 0 ? 4 : 2;
-        if (t.offset > data_.size() || data_off_ + t.offset + (size_t) t.n * esz > data_.size()) {
-            err = path + ": tensor " + t.name + " out of bounds";
-            return false;
+        tensor &t = tensors[i];
+        uint32_t nd;
+        if (!r.text(t.name) || !r.scalar(nd)) return bad("truncated tensor info section");
+        if (nd > 8) return bad("corrupt tensor info");
+        uint64_t n = 1;
+        bool too_big = false;
+        t.dims.resize(nd);
+        for (auto &d : t.dims) {
+            if (!r.scalar(d)) return bad("truncated tensor info section");
+            too_big = too_big || __builtin_mul_overflow(n, d, &n);
         }
-        index[t.name] = i;
+        if (!r.scalar(t.type) || !r.scalar(t.offset)) return bad("truncated tensor info section");
+        if (t.type > 1) return bad("tensor " + t.name + " has unsupported type");
+        // 2^60 elements of at most 4 bytes keep every byte count below 2^64
+        if (too_big || n > ((uint64_t) 1 << 60)) return bad("tensor " + t.name + " out of bounds");
+        t.n = (int64_t) n;
+        if (!index_.emplace(t.name, i).second) return bad("duplicate tensor " + t.name);
+    }
+    // the data section starts at the next multiple of the alignment
+    data_start_ = (r.pos() + align - 1) / align * align;
+    const uint64_t avail = size_ > data_start_ ? size_ - data_start_ : 0;
+    for (const tensor &t : tensors) {
+        const uint64_t bytes = (uint64_t) t.n * (t.type == 0 ? 4 : 2);
+        if (t.offset > avail || bytes > avail - t.offset) return bad("tensor " + t.name + " out of bounds");
     }
     return true;
 }
 
 const gguf_file::tensor *gguf_file::find(const std::string &name) const {
-    auto it = index.find(name);
-    return it == index.end() ? nullptr : &tensors[it->second];
+    auto it = index_.find(name);
+    return it == index_.end() ? nullptr : &tensors[it->second];
 }
 
 bool gguf_file::read(const std::string &name, std::vector<float> &out, bool &f16, std::string &err) const {
@@ -187,17 +270,13 @@ bool gguf_file::read(const std::string &name, std::vector<float> &out, bool &f16
         err = "missing tensor " + name;
         return false;
     }
-    const uint8_t *src = data_.data() + data_off_ + t->offset;
+    const uint8_t *src = base_ + data_start_ + t->offset;  // in bounds: checked by open()
     out.resize((size_t) t->n);
     f16 = t->type == 1;
     if (!f16) {
-        memcpy(out.data(), src, (size_t) t->n * 4);
+        if (t->n) memcpy(out.data(), src, (size_t) t->n * 4);
     } else {
-        for (int64_t j = 0; j < t->n; j++) {
-            uint16_t h;
-            memcpy(&h, src + 2 * j, 2);
-            out[(size_t) j] = half_to_float(h);
-        }
+        for (int64_t j = 0; j < t->n; j++) out[(size_t) j] = half_to_float(load_le<uint16_t>(src + 2 * j));
     }
     return true;
 }
@@ -209,143 +288,3 @@ bool gguf_weight_source::get(const std::string &name, std::vector<float> &data, 
 
 }  // namespace tp
 
-// ---------------------------------------------------------------------------
-extern "C" {
-
-int tpmd_load_gguf(tpmd_ctx *ctx, const char *path, char *err, size_t err_size) {
-    auto fail = [&](const std::string &m) {
-        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
-        return -1;
-    };
-    if (!ctx || !path) return fail("tpmd_load_gguf: null context or path");
-    tp::gguf_file f;
-    std::string e;
-    if (!f.open(path, "float-motion-ae", e)) return fail(e);
-    std::vector<float> v;
-    for (int i = 0;; i++) {
-        int64_t n = 0;
-        const char *name = tpmd_weight_name(ctx, i, &n, nullptr);
-        if (!name) break;
-        if (!f.find(name)) continue;  // prepare() names the first missing tensor
-        bool f16 = false;
-        if (!f.read(name, v, f16, e)) return fail(e);
-        if ((int64_t) v.size() != n)
-            return fail(std::string(path) + ": tensor " + name + " has " + std::to_string(v.size()) +
-                        " elements, expected " + std::to_string(n));
-        if (tpmd_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
-            return fail(tpmd_last_error(ctx));
-    }
-    return 0;
-}
-
-int tpme_load_gguf(tpme_ctx *ctx, const char *path, char *err, size_t err_size) {
-    auto fail = [&](const std::string &m) {
-        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
-        return -1;
-    };
-    if (!ctx || !path) return fail("tpme_load_gguf: null context or path");
-    tp::gguf_file f;
-    std::string e;
-    if (!f.open(path, "float-motion-ae", e)) return fail(e);
-    std::vector<float> v;
-    for (int i = 0;; i++) {
-        int64_t n = 0;
-        const char *name = tpme_weight_name(ctx, i, &n, nullptr);
-        if (!name) break;
-        if (!f.find(name)) continue;  // prepare() names the first missing tensor
-        bool f16 = false;
-        if (!f.read(name, v, f16, e)) return fail(e);
-        if ((int64_t) v.size() != n)
-            return fail(std::string(path) + ": tensor " + name + " has " + std::to_string(v.size()) +
-                        " elements, expected " + std::to_string(n));
-        if (tpme_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
-            return fail(tpme_last_error(ctx));
-    }
-    return 0;
-}
-
-int tpfm_read_config(const char *path, tpfm_config *cfg, char *err, size_t err_size) {
-    auto fail = [&](const std::string &m) {
-        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
-        return -1;
-    };
-    if (!path || !cfg) return fail("tpfm_read_config: null path or config");
-    tp::gguf_file f;
-    std::string e;
-    if (!f.open(path, "float-fmt", e)) return fail(e);
-    tpfm_default_config(cfg);
-    auto num = [&](const char *key, double def) {
-        auto it = f.kv_num.find(std::string("float.fmt.") + key);
-        return it == f.kv_num.end() ? def : it->second;
-    };
-    // src/fmt.cpp:10-26
-    cfg->dim_h = (int) num("dim_h", cfg->dim_h);
-    cfg->depth = (int) num("depth", cfg->depth);
-    cfg->n_heads = (int) num("n_heads", cfg->n_heads);
-    cfg->dim_w = (int) num("dim_w", cfg->dim_w);
-    cfg->dim_a = (int) num("dim_a", cfg->dim_a);
-    cfg->dim_e = (int) num("dim_e", cfg->dim_e);
-    cfg->chunk_frames = (int) num("chunk_frames", cfg->chunk_frames);
-    cfg->prev_frames = (int) num("prev_frames", cfg->prev_frames);
-    cfg->attn_window = (int) num("attn_window", cfg->attn_window);
-    cfg->t_freq_dim = (int) num("t_freq_dim", cfg->t_freq_dim);
-    cfg->nfe = (int) num("nfe", cfg->nfe);
-    cfg->a_cfg = (float) num("a_cfg_scale", cfg->a_cfg);
-    cfg->e_cfg = (float) num("e_cfg_scale", cfg->e_cfg);
-    cfg->r_cfg = (float) num("r_cfg_scale", cfg->r_cfg);
-    cfg->ln_eps = (float) num("ln_eps", cfg->ln_eps);
-    cfg->mlp_ratio = (float) num("mlp_ratio", cfg->mlp_ratio);
-    const double total = num("num_total_frames", cfg->chunk_frames + cfg->prev_frames);
-    if ((int) total != cfg->chunk_frames + cfg->prev_frames)
-        return fail(std::string(path) + ": num_total_frames != chunk_frames + prev_frames");
-    return 0;
-}
-
-int tpfm_load_gguf(tpfm_ctx *ctx, const char *path, char *err, size_t err_size) {
-    auto fail = [&](const std::string &m) {
-        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
-        return -1;
-    };
-    if (!ctx || !path) return fail("tpfm_load_gguf: null context or path");
-    tp::gguf_file f;
-    std::string e;
-    if (!f.open(path, "float-fmt", e)) return fail(e);
-    std::vector<float> v;
-    for (int i = 0;; i++) {
-        int64_t n = 0;
-        const char *name = tpfm_weight_name(ctx, i, &n, nullptr);
-        if (!name) break;
-        if (!f.find(name)) continue;  // prepare() names the first missing tensor
-        bool f16 = false;
-        if (!f.read(name, v, f16, e)) return fail(e);
-        if ((int64_t) v.size() != n)
-            return fail(std::string(path) + ": tensor " + name + " has " + std::to_string(v.size()) +
-                        " elements, expected " + std::to_string(n));
-        if (tpfm_set_weight(ctx, name, v.data(), n, f16 ? TPMD_W_F16_FILE : 0) != 0)
-            return fail(tpfm_last_error(ctx));
-    }
-    return 0;
-}
-
-int64_t tpmd_gguf_read_tensor(const char *path, const char *name, float *out, int64_t cap, int *is_f16,
-                              char *err, size_t err_size) {
-    auto fail = [&](const std::string &m) -> int64_t {
-        if (err && err_size) snprintf(err, err_size, "%s", m.c_str());
-        return -1;
-    };
-    if (!path || !name) return fail("tpmd_gguf_read_tensor: null path or name");
-    tp::gguf_file f;
-    std::string e;
-    if (!f.open(path, nullptr, e)) return fail(e);
-    std::vector<float> v;
-    bool f16 = false;
-    if (!f.read(name, v, f16, e)) return fail(e);
-    if (is_f16) *is_f16 = f16 ? 1 : 0;
-    if (out) {
-        if (cap < (int64_t) v.size()) return fail("tpmd_gguf_read_tensor: buffer too small");
-        memcpy(out, v.data(), v.size() * 4);
-    }
-    return (int64_t) v.size();
-}
-
-}  // extern "C"

@@ -1,11 +1,13 @@
-"""Minimal GGUF v3 writer for tests (little-endian, per the GGUF v3 layout the
-reference's loader reads, src/gguf_load.cpp:51-197): KV strings / u32, tensor
-dims in ggml order (reversed torch shape), F32 or F16 data, 32-byte aligned."""
+"""Minimal GGUF v3 writer for tests (little-endian, the GGUF v3 layout: header,
+metadata key/value pairs of any of the 13 value types, tensor records with
+dims in ggml order (reversed torch shape), F32 or F16 data aligned to 32
+bytes or general.alignment)."""
 import struct
 
 import numpy as np
 
 ALIGN = 32
+_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
 
 
 def _s(b, text):
@@ -13,41 +15,56 @@ def _s(b, text):
     b += struct.pack("<Q", len(raw)) + raw
 
 
+def _value(b, vt, val):
+    if vt == 8:
+        _s(b, val)
+    elif vt == 9:                       # (element type, [values])
+        et, items = val
+        b += struct.pack("<IQ", et, len(items))
+        for it in items:
+            _value(b, et, it)
+    else:
+        b += struct.pack(_FMT[vt], val)
+
+
 def write(path, tensors, arch="float-motion-ae", f16=False, extra_kv=None, version=3,
-          bad_type=None):
+          bad_type=None, dims_override=None, duplicate=None, align=None):
     """tensors: {name: (array in torch shape, store_f16)}; f16=True stores every
-    tensor flagged store_f16 as F16.  bad_type: a tensor name written with
-    type 8 (unsupported)."""
+    tensor flagged store_f16 as F16.  extra_kv: [(key, value type, value)].
+    bad_type: a tensor name written with type 8 (unsupported).
+    dims_override: {name: dims} written instead of the array's (the data stays
+    the array's).  duplicate: a tensor name whose record is written twice.
+    align: a general.alignment to write and lay the data out with."""
     kv = [("general.architecture", 8, arch)] if arch is not None else []
+    if align is not None:
+        kv.append(("general.alignment", 4, align))
     kv += list(extra_kv or [])
-    head = bytearray(b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(kv)))
+    al = align or ALIGN
+    recs = list(tensors.items())
+    if duplicate is not None:
+        recs.append((duplicate, tensors[duplicate]))
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", version, len(recs), len(kv)))
     for key, vt, val in kv:
         _s(head, key)
         head += struct.pack("<I", vt)
-        if vt == 8:
-            _s(head, val)
-        elif vt == 4:
-            head += struct.pack("<I", val)
-        elif vt == 6:
-            head += struct.pack("<f", val)
-        else:
-            raise ValueError(vt)
-    blobs, off = [], 0
+        _value(head, vt, val)
+    blobs, off, offs = [], 0, {}
     for name, (arr, store16) in tensors.items():
         a = np.ascontiguousarray(arr, np.float32)
-        use16 = f16 and store16
-        data = (a.astype(np.float16) if use16 else a).tobytes()
-        _s(head, name)
-        dims = list(reversed(a.shape)) or [1]
-        head += struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims)
-        gtype = 8 if name == bad_type else (1 if use16 else 0)
-        head += struct.pack("<IQ", gtype, off)
+        data = (a.astype(np.float16) if f16 and store16 else a).tobytes()
+        offs[name] = off
         blobs.append(data)
         off += len(data)
-        off = (off + ALIGN - 1) // ALIGN * ALIGN
-    pad = (-len(head)) % ALIGN
+        off = (off + al - 1) // al * al
+    for name, (arr, store16) in recs:
+        _s(head, name)
+        dims = (dims_override or {}).get(name) or list(reversed(np.shape(arr))) or [1]
+        head += struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims)
+        gtype = 8 if name == bad_type else (1 if f16 and store16 else 0)
+        head += struct.pack("<IQ", gtype, offs[name])
+    pad = (-len(head)) % al
     out = bytes(head) + b"\0" * pad
     for d in blobs:
-        out += d + b"\0" * ((-len(d)) % ALIGN)
+        out += d + b"\0" * ((-len(d)) % al)
     with open(path, "wb") as f:
         f.write(out)
