@@ -229,6 +229,21 @@ int tpmd_stage_times(const tpmd_ctx *ctx, float *us, int max_slots);
 int tpmd_modconv(tpmd_ctx *ctx, int conv, const float *x, int n, int H, int W, const float *s,
                  float *y, void *stream);
 
+/* tpmd_modconv for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, kernels
+ * and results as tpmd_modconv, but its scratch (the style-multiplied
+ * input, 1/den, split-K partial sums; each rounded up to 256 bytes) lives
+ * in a static device array of TPMD_STATIC_SCRATCH_BYTES per GPU, resolved
+ * when a context is created on that GPU and held until the process ends;
+ * the call allocates nothing.  A call whose scratch exceeds it fails
+ * ("needs N bytes of scratch").  All calls on one GPU share the array, from
+ * every context: calls that overlap on one GPU (different streams, or
+ * contexts used from several threads) race. */
+#define TPMD_STATIC_SCRATCH_BYTES ((size_t) 16 << 20)
+int tpmd_modconv_static(tpmd_ctx *ctx, int conv, const float *x, int n, int H, int W, const float *s,
+                        float *y, void *stream);
+
 /* Stage tail of stage j (src/motion_dec.cpp:1077-1108): ToFlow (+ flow
  * skip), flow head, grid_sample warp of feats j, warp/trunk blend, ToRGB
  * (+ rgb skip).  out: CL [n][r][r][C] dense-conv output; s_flow: [n][C];

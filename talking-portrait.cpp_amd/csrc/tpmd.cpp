@@ -32,7 +32,37 @@
 
 using namespace tpmd;
 
+// The scratch of tpmd_modconv_static, one array per GPU, held by every GPU the
+// library runs on until the process ends.  On the host the name is only a
+// stand-in for the symbol: each device's address comes from
+// hipGetSymbolAddress (static_scratch_of), and only that address is used.
+static __device__ __align__(256) char scratch[TPMD_STATIC_SCRATCH_BYTES];
+
 namespace {
+
+// the device address of `scratch` on `device`, which must be current;
+// resolved on the first call for each device and kept (null + reason in err
+// on failure)
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void *scratch_dev[kMaxDevices] = {};
+void *static_scratch_of(int device, std::string &err) {
+    if (device < 0 || device >= kMaxDevices) {
+        err = "device ordinal out of range";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    if (!scratch_dev[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            err = std::string("hipGetSymbolAddress: ") + hipGetErrorString(e);
+            return nullptr;
+        }
+        scratch_dev[device] = p;
+    }
+    return scratch_dev[device];
+}
 
 const int REF_IC[7] = {512, 512, 512, 512, 256, 128, 64};
 const int REF_OC[7] = {512, 512, 512, 256, 128, 64, 32};
@@ -217,6 +247,9 @@ struct tpmd_ctx {
     // scratch for the per-stage entry points (grow-only)
     void *scr[4] = {};
     size_t scr_sz[4] = {};
+    // this device's static scratch (tpmd_modconv_static), or null + reason
+    void *static_scratch = nullptr;
+    std::string static_scratch_err;
 
     bool profile = false;
 
@@ -597,6 +630,7 @@ static tpmd_ctx *tpmd_create_body(int device, const char *ftype, int n_stages, c
         return nullptr;
     }
     c->stream = c->own_stream;
+    c->static_scratch = static_scratch_of(device, c->static_scratch_err);
     return c;
 }
 
@@ -1339,23 +1373,40 @@ static int tpmd_set_tap_body(tpmd_ctx *c, int kind, int stage, void *dst, int64_
     return 0;
 }
 
-static int tpmd_modconv_body(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
-                 void *stream) {
-    if (!check_ctx(c)) return -1;
+// argument checks of tpmd_modconv / tpmd_modconv_static
+static bool modconv_args_ok(tpmd_ctx *c, const char *who, int conv, const float *x, int n, int H, int W,
+                            const float *s, const float *y) {
     if (!c->prepared) {
         c->err = "decoder not prepared";
-        return -1;
+        return false;
     }
     if (conv < 0 || conv >= c->nconv || !x || !s || !y || n < 1 || H < 1 || W < 1) {
-        c->err = "tpmd_modconv: bad arguments";
-        return -1;
+        c->err = std::string(who) + ": bad arguments";
+        return false;
     }
-    const ConvW &cv = c->conv[conv];
-    hipStream_t st = pick_stream(c, stream);
+    return true;
+}
+
+// device scratch of one tpmd_modconv call: the input multiplied by the style
+// (the conv's operand type), 1/den, and the split-K partial sums (0 bytes
+// when the conv shape runs unsplit)
+struct ModconvScratch {
+    size_t xs = 0, den = 0, ws = 0;
+    static size_t up256(size_t b) { return (b + 255) & ~(size_t) 255; }
+    size_t total() const { return up256(xs) + up256(den) + up256(ws); }
+};
+static ModconvScratch modconv_scratch(const tpmd_ctx *c, const ConvW &cv, int n, int H, int W) {
+    ModconvScratch m;
+    m.xs = (size_t) n * H * W * cv.ic * c->act_size();
+    m.den = (size_t) n * cv.oc * 4;
+    m.ws = (size_t) modconv_ws_elems(cv.up ? 1 : 0, n, H, W, cv.ic, cv.oc, c->f16) * 4;
+    return m;
+}
+
+// demodulation, style multiply and the conv of tpmd_modconv on given scratch
+static int modconv_run(tpmd_ctx *c, const ConvW &cv, const float *x, int n, int H, int W, const float *s, float *y,
+                       hipStream_t st, void *xs, float *den, float *ws) {
     const int64_t npix = (int64_t) H * W;
-    void *xs = c->scratch(1, (size_t) n * npix * cv.ic * c->act_size());
-    float *den = (float *) c->scratch(2, (size_t) n * cv.oc * 4);
-    if (!xs || !den) return -1;
     DemodTable t{};
     t.n = 1;
     t.row0[0] = 0;
@@ -1383,12 +1434,42 @@ static int tpmd_modconv_body(tpmd_ctx *c, int conv, const float *x, int n, int H
     ca.OC = cv.oc;
     ca.x_bstride = npix * cv.ic;
     ca.ws_elems = modconv_ws_elems(ca.mode, n, H, W, cv.ic, cv.oc, c->f16);
-    if (ca.ws_elems > 0) {
-        ca.ws = (float *) c->scratch(3, (size_t) ca.ws_elems * 4);
-        if (!ca.ws) return -1;
+    ca.ws = ca.ws_elems > 0 ? ws : nullptr;
+    return c->hip_ok(launch_modconv(ca, st), "modconv") ? 0 : -1;
+}
+
+static int tpmd_modconv_body(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
+                             void *stream) {
+    if (!check_ctx(c) || !modconv_args_ok(c, "tpmd_modconv", conv, x, n, H, W, s, y)) return -1;
+    const ConvW &cv = c->conv[conv];
+    const ModconvScratch m = modconv_scratch(c, cv, n, H, W);
+    void *xs = c->scratch(1, m.xs);
+    float *den = (float *) c->scratch(2, m.den);
+    float *ws = m.ws ? (float *) c->scratch(3, m.ws) : nullptr;
+    if (!xs || !den || (m.ws && !ws)) return -1;
+    return modconv_run(c, cv, x, n, H, W, s, y, pick_stream(c, stream), xs, den, ws);
+}
+
+static int tpmd_modconv_static_body(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s,
+                                    float *y, void *stream) {
+    if (!check_ctx(c) || !modconv_args_ok(c, "tpmd_modconv_static", conv, x, n, H, W, s, y)) return -1;
+    if (!c->static_scratch) {
+        c->err = "tpmd_modconv_static: the static scratch of this device is unavailable (" +
+                 c->static_scratch_err + ")";
+        return -1;
     }
-    if (!c->hip_ok(launch_modconv(ca, st), "modconv")) return -1;
-    return 0;
+    const ConvW &cv = c->conv[conv];
+    const ModconvScratch m = modconv_scratch(c, cv, n, H, W);
+    if (m.total() > TPMD_STATIC_SCRATCH_BYTES) {
+        c->err = fmt("tpmd_modconv_static: this call needs %zu bytes of scratch, the static scratch holds %zu",
+                     m.total(), (size_t) TPMD_STATIC_SCRATCH_BYTES);
+        return -1;
+    }
+    char *base = (char *) c->static_scratch;
+    void *xs = base;
+    float *den = (float *) (base + ModconvScratch::up256(m.xs));
+    float *ws = m.ws ? (float *) (base + ModconvScratch::up256(m.xs) + ModconvScratch::up256(m.den)) : nullptr;
+    return modconv_run(c, cv, x, n, H, W, s, y, pick_stream(c, stream), xs, den, ws);
 }
 
 static int tpmd_stage_tail_body(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
@@ -1593,6 +1674,11 @@ int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
 int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
                  void *stream) {
     return guarded(c, [&] { return tpmd_modconv_body(c, conv, x, n, H, W, s, y, stream); });
+}
+
+int tpmd_modconv_static(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
+                        void *stream) {
+    return guarded(c, [&] { return tpmd_modconv_static_body(c, conv, x, n, H, W, s, y, stream); });
 }
 
 int tpmd_stage_tail(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,

@@ -75,6 +75,7 @@ def lib():
             "tpmd_set_tap": (I, [P, I, I, P, I64]),
             "tpmd_tap_frame_bytes": (I64, [P, I, I]),
             "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
+            "tpmd_modconv_static": (I, [P, I, P, I, I, I, P, P, P]),
             "tpmd_stage_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P]),
             "tpmd_stage_conv_tail": (I, [P, I, P, I, P, P, P, P, P, P, P, P, P]),
             "tpmd_gather": (I, [P, I, I, I, I, P, I64, I, I, P, P]),
@@ -317,6 +318,12 @@ class MotionDecoder:
     def modconv(self, conv, x, s, y, stream=None):
         n, H, W, _ = x.shape
         self._check(lib().tpmd_modconv(self.h, conv, _ptr(x), n, H, W, _ptr(s), _ptr(y), _stream(stream)))
+
+    def modconv_static(self, conv, x, s, y, stream=None):
+        """modconv on the library's static device scratch (allocates nothing)"""
+        n, H, W, _ = x.shape
+        self._check(lib().tpmd_modconv_static(self.h, conv, _ptr(x), n, H, W, _ptr(s), _ptr(y),
+                                              _stream(stream)))
 
     def stage_tail(self, j, out, s_flow, flow_prev, rgb_prev, flow, trunk, rgb, warp, stream=None):
         n = out.shape[0]
