@@ -68,10 +68,16 @@ def stage_costs(ic, oc, nframes, ftype):
     sa = 2 if ftype == "f16" else 4   # conv operand / activation bytes
     sw = sa                            # conv weight bytes
     C0 = ic[0]
-    # style GEMV + demod + conv1: latents, modulation weights, conv1 weights
-    # and its output; FLOPs of conv1 only
-    f0 = 2 * nframes * 16 * 9 * C0 * C0
-    b0 = nframes * 512 * 4 + 9 * C0 * C0 * sw + nframes * 16 * C0 * sa
+    # style GEMV + demod + conv1: latents; the modulation weights of all 22
+    # modulated convs (f32 rows of 512, one per input channel); S_aug of the
+    # 15 demodulated convs ([OC][IC + 1] f32); conv1 weights and its output.
+    # FLOPs: conv1, the style GEMVs and the demodulations
+    convs = [(C0, C0)] + [(c_in, oc[j]) for j in range(len(ic)) for c_in in (ic[j], oc[j])]
+    mod_rows = sum(c_in for c_in, _ in convs) + sum(oc)
+    saug = sum(o * (c_in + 1) for c_in, o in convs)
+    f0 = 2 * nframes * 16 * 9 * C0 * C0 + 2 * nframes * 512 * mod_rows + 2 * nframes * saug
+    b0 = (nframes * 512 * 4 + mod_rows * 512 * 4 + saug * 4 + 9 * C0 * C0 * sw
+          + nframes * 16 * C0 * sa)
     slots = [("style+conv1", f0, b0)]
     for j in range(len(ic)):
         r = 8 << j
@@ -158,8 +164,7 @@ def fmt_timing(ftype, reps=5):
     import numpy as np
     import synth
     import tpmd
-    from oracle import fmt as OF   # names and shapes only (the tensor list)
-    cfg = OF.Config()
+    cfg = synth.FmtConfig()
     fm = tpmd.FlowTransformer(ftype)
     fm.set_weights(synth.fmt_raw_weights(cfg, ftype=ftype))
     fm.prepare()
@@ -273,27 +278,49 @@ def gather_timing(reps=50):
     return rows
 
 
+def cpu_topology():
+    """(logical CPUs this process may run on, physical cores among them),
+    from the kernel's CPU topology"""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    return len(cpus), len(cores)
+
+
 def cpu_baseline(ftype_unused=None):
     """the CPU oracle's fast graph (f32, numpy/OpenBLAS + OpenMP C ops) on
-    this host, one 512x512 frame"""
+    this host, timed with tp-bench's mdec protocol (bench/tp-bench.cpp:
+    136-151): batches of 8 frames, two untimed warm-up batches, then
+    iters * 5 timed batches (iters = 1 here, a bounded sample), ms per frame
+    = total / (batches * 8); threads = the physical cores (the reference's
+    best CPU setting, docs/r3-summary.md:29-31)"""
+    from threadpoolctl import threadpool_limits
     from oracle import mdec as om
     import synth
-    threads = len(os.sched_getaffinity(0))
-    om.set_threads(threads)
-    raw, lat, feats = synth.workload("iid", 2, "f32")
+    logical, physical = cpu_topology()
+    om.set_threads(physical)
+    B, iters = 8, 1
+    raw, lat, feats = synth.workload("iid", B, "f32")
     dec = om.Decoder(raw, "f32")
     dec.set_feats(feats)
-    dec.decode_fast(lat[:1])          # warm-up (page-in, BLAS init)
-    t0 = time.perf_counter()
-    n = 0
-    while True:
-        dec.decode_fast(lat[n % 2: n % 2 + 1])
-        n += 1
-        if time.perf_counter() - t0 > 10.0 or n >= 8:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 4), "unit": "frames/s", "cores": threads, "kind": "port",
-            "sample": f"{n} frame(s) of the f32 fast-graph oracle at 512x512, i.i.d. workload"}
+    with threadpool_limits(limits=physical):
+        for _ in range(2):
+            dec.decode_fast(lat)
+        t0 = time.perf_counter()
+        for _ in range(iters * 5):
+            dec.decode_fast(lat)
+        dt = time.perf_counter() - t0
+    n = iters * 5 * B
+    return {"value": round(n / dt, 4), "unit": "frames/s", "cores": physical, "kind": "port",
+            "physical_cores": physical, "logical_cpus": logical,
+            "sample": f"tp-bench mdec protocol: {iters * 5} timed batches of {B} frames after 2 warm-up batches, "
+                      f"f32 fast-graph oracle at 512x512, i.i.d. workload, {physical} threads "
+                      f"(physical cores of the {logical} logical CPUs available)"}
 
 
 def main():
@@ -310,6 +337,8 @@ def main():
                          "one stream (kernel traces comparable with the per-stage events)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run the 256 MiB calibration copy (for counter runs)")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="skip the frame-path, encoder, FMT and gather legs (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -331,14 +360,16 @@ def main():
     dec.build(B)
     dec.set_feats(feats)
     lat_dev = torch.from_numpy(np.concatenate([lat, lat[:B]])).cuda()   # wrap-around window
-    imgs = torch.empty((B, 3, 512, 512), dtype=torch.float32, device="cuda")
+    # one frame buffer per decoder lane: consecutive calls overlap on the GPU,
+    # and a call writing a buffer that an in-flight call writes would wait
+    imgs_ring = [torch.empty((B, 3, 512, 512), dtype=torch.float32, device="cuda") for _ in range(3)]
     torch.cuda.synchronize()   # inputs resident before the decoder stream reads them
     if args.lanes == 1:
         dec.use_stream(torch.cuda.current_stream())   # a caller's stream: one lane
 
     def step(k):
         t0 = (k * B) % n_seq
-        dec.decode_batch_device(lat_dev[t0:t0 + B], imgs)
+        dec.decode_batch_device(lat_dev[t0:t0 + B], imgs_ring[k % 3])
 
     for k in range(args.warmup):
         step(k)
@@ -379,7 +410,7 @@ def main():
         "ms_per_step": round(dt / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(fps / REF_FPS_RTX5070TI, 3) if args.ftype == "f16" else None,
+        "vs_baseline": None,   # set below from the rate that includes the download, as the reference's does
         "dtype": "f16" if args.ftype == "f16" else "f32",
         "data": "synthetic",
         "config": {"workload": f"LIA motion decoder 512x512, {n_seq}-frame AR(1) latent sequence "
@@ -391,6 +422,11 @@ def main():
         "stage_sum_us": round(float(us.sum()), 1),
         "lanes": args.lanes,
     }
+    if args.decoder_only:
+        if args.copy_probe:
+            copy_probe()
+        print(json.dumps(out))
+        return
     # the clip delivered to host memory through the frame output path
     # (downloads overlapped with decoding): reported beside `value`, never as it
     host = {}
@@ -410,6 +446,14 @@ def main():
         del buf
     out["host_delivered_fps"] = {"frames": n_seq, **host,
                                  "note": "host buffers (pageable, or pinned where named), PCIe download included"}
+    # the reference's figure times decode_batch into a host std::vector, the
+    # f32 download included (bench/tp-bench.cpp:133-151): compare like with like
+    if args.ftype == "f16":
+        out["vs_baseline"] = round(host["f32_chw"] / REF_FPS_RTX5070TI, 3)
+        out["vs_baseline_basis"] = ("host_delivered_fps.f32_chw (f32 CHW frames in pageable host memory) / "
+                                    f"{REF_FPS_RTX5070TI} frames/s (GGML-CUDA f16 mdec, RTX 5070 Ti, "
+                                    "docs/vulkan-perf.md:134)")
+        out["device_resident_vs_reference"] = round(fps / REF_FPS_RTX5070TI, 3)
     out["encoder"] = encoder_timing(args.ftype)
     out["fmt"] = fmt_timing(args.ftype)
     out["gather"] = gather_timing()

@@ -109,7 +109,7 @@ def f16_bits(x):
 
 def leaky(v):
     v = _f32(v)
-    return np.where(v > 0, v, np.float32(SLOPE) * v).astype(np.float32)
+    return np.where(v > 0, v, np.float32(SLOPE) * v).astype(np.float32, copy=False)
 
 
 def bilinear_gather(feat, grid, W, H, planar=False, sp=False):
@@ -254,7 +254,7 @@ def conv2d_s(x, w, stride, pad):
 def mul_mat(a, b):
     """ggml_mul_mat(a [K, M], b [K, N]) -> [M, N]; numpy a (..., M, K),
     b (..., N, K) -> (..., N, M), f32 accumulation."""
-    return np.matmul(_f32(b), np.swapaxes(_f32(a), -1, -2)).astype(np.float32)
+    return np.matmul(_f32(b), np.swapaxes(_f32(a), -1, -2)).astype(np.float32, copy=False)
 
 
 def set_threads(n):
@@ -338,7 +338,7 @@ def load_weights(raw, keep_f16):
             a = round_f16(a)  # the file holds f16 values
         s = motion_ae_scale(name, ggml_ne(a.shape))
         if s != 1.0:
-            a = (a * np.float32(s)).astype(np.float32)
+            a = (a * np.float32(s)).astype(np.float32, copy=False)
         host[name] = a
         big = keep_f16 and f16_in_file and a.size >= 4096
         isf16[name] = big
@@ -413,18 +413,18 @@ class Decoder:
         latent (B, 512) -> (B, IC)."""
         mw = self.w[base + ".modulation.weight"]
         mb = self.w[base + ".modulation.bias"].reshape(-1)
-        return (mul_mat(mw, latent) + mb).astype(np.float32)
+        return (mul_mat(mw, latent) + mb).astype(np.float32, copy=False)
 
     def demod_den(self, wname, s):
         """sqrt(S_aug . [s^2; 1]) (src/motion_dec.cpp:275-280): (B, OC)."""
         sa = self.der["saug." + wname]
         s2 = np.concatenate([_f32(s) * _f32(s), np.ones((s.shape[0], 1), np.float32)], axis=1)
-        return np.sqrt(mul_mat(sa, s2)).astype(np.float32)
+        return np.sqrt(mul_mat(sa, s2)).astype(np.float32, copy=False)
 
     @staticmethod
     def lin(r):
         i = np.arange(r, dtype=np.float64)
-        return (-1.0 + 2.0 * i / (r - 1)).astype(np.float32)
+        return (-1.0 + 2.0 * i / (r - 1)).astype(np.float32, copy=False)
 
     # ------------------------------------------------------------------
     # exact (parity) graph, one frame, f32 (src/motion_dec.cpp:794-888)
@@ -434,9 +434,9 @@ class Decoder:
         den = self.demod_den(base + ".conv.weight", s[None])[0]
         W = self.w[base + ".conv.weight"].reshape(den.size, s.size, 3, 3)
         ab = self.w[base + ".activate.bias"].reshape(-1)
-        xs = (x * s[:, None, None]).astype(np.float32)
+        xs = (x * s[:, None, None]).astype(np.float32, copy=False)
         y = conv2d_direct(xs, W, 1)
-        y = (y / den[:, None, None]).astype(np.float32)
+        y = (y / den[:, None, None]).astype(np.float32, copy=False)
         return leaky(y + ab[:, None, None])
 
     def _styled_conv_up_exact(self, x, base, latent):
@@ -446,11 +446,11 @@ class Decoder:
         kb = self.w[base + ".conv.blur.kernel"].reshape(4, 4)
         ab = self.w[base + ".activate.bias"].reshape(-1)
         C, H, W = x.shape
-        xs = (x * s[:, None, None]).astype(np.float32)
+        xs = (x * s[:, None, None]).astype(np.float32, copy=False)
         zs = np.zeros((C, 2 * H + 3, 2 * W + 3), np.float32)   # zero_stuff2 + pad(2,1)
         zs[:, 2:2 * H + 2:2, 2:2 * W + 2:2] = xs
         y = conv2d_direct(zs, Wf, 0)                           # (OC, 2H+1, 2W+1)
-        y = (y / den[:, None, None]).astype(np.float32)
+        y = (y / den[:, None, None]).astype(np.float32, copy=False)
         OC = y.shape[0]
         yp = np.zeros((OC, 2 * H + 3, 2 * W + 3), np.float32)  # blur pad (1,1)
         yp[:, 1:-1, 1:-1] = y
@@ -481,33 +481,33 @@ class Decoder:
             fb = f"dec.to_flows.{j}"
             fs = self.style_of(fb + ".conv", latent[None])[0]
             fW = self.w[fb + ".conv.weight"].reshape(3, -1, 1, 1)
-            xs = (out * fs[:, None, None]).astype(np.float32)
+            xs = (out * fs[:, None, None]).astype(np.float32, copy=False)
             fl = conv2d_direct(xs, fW, 0) + self.w[fb + ".bias"].reshape(3, 1, 1)
-            fl = fl.astype(np.float32)
+            fl = fl.astype(np.float32, copy=False)
             if skip_flow is not None:
-                fl = (fl + upfirdn2x(skip_flow, self.w[fb + ".upsample.kernel"])).astype(np.float32)
+                fl = (fl + upfirdn2x(skip_flow, self.w[fb + ".upsample.kernel"])).astype(np.float32, copy=False)
             skip_flow = fl
             taps[f"r{r}.flowmap"] = fl
             lin = self.lin(r)
-            gx = (tanh(fl[0]) + lin[None, :]).astype(np.float32)
-            gy = (tanh(fl[1]) + lin[:, None]).astype(np.float32)
+            gx = (tanh(fl[0]) + lin[None, :]).astype(np.float32, copy=False)
+            gy = (tanh(fl[1]) + lin[:, None]).astype(np.float32, copy=False)
             taps[f"r{r}.grid"] = np.stack([gx, gy], axis=-1)
             m = sigmoid(fl[2])
             grid = np.stack([gx.reshape(-1), gy.reshape(-1)], axis=1)
             sampled = bilinear_gather(self.feats[j], grid, r, r)        # (N, C)
             sampled = np.ascontiguousarray(sampled.T.reshape(-1, r, r))  # cl_to_sp
-            warp = (sampled * m[None]).astype(np.float32)
+            warp = (sampled * m[None]).astype(np.float32, copy=False)
             taps[f"r{r}.warp"] = warp
-            one_m = (np.float32(1.0) - m).astype(np.float32)
-            trunk = (warp + (out * one_m[None]).astype(np.float32)).astype(np.float32)
+            one_m = (np.float32(1.0) - m).astype(np.float32, copy=False)
+            trunk = (warp + (out * one_m[None]).astype(np.float32, copy=False)).astype(np.float32, copy=False)
             taps[f"r{r}.out"] = trunk
             rb = f"dec.to_rgbs.{j}"
             rW = self.w[rb + ".conv.0.weight"].reshape(3, -1, 1, 1)
             rgb = conv2d_direct(warp, rW, 0)
             rgb = leaky(rgb + self.w[rb + ".conv.1.bias"].reshape(3, 1, 1))
-            rgb = (rgb + self.w[rb + ".bias"].reshape(3, 1, 1)).astype(np.float32)
+            rgb = (rgb + self.w[rb + ".bias"].reshape(3, 1, 1)).astype(np.float32, copy=False)
             if skip is not None:
-                rgb = (rgb + upfirdn2x(skip, self.w[rb + ".upsample.kernel"])).astype(np.float32)
+                rgb = (rgb + upfirdn2x(skip, self.w[rb + ".upsample.kernel"])).astype(np.float32, copy=False)
             skip = rgb
             taps[f"r{r}.rgb"] = rgb
             out = trunk
@@ -531,8 +531,8 @@ class Decoder:
         IC = s.shape[1]
         R = A.shape[1]
         sty = np.tile(s, (1, R // IC))                       # (B, R)
-        Af = (A[None] * sty[:, None, :]).astype(np.float32)
-        Af = (Af / den[:, :, None]).astype(np.float32)
+        Af = (A[None] * sty[:, None, :]).astype(np.float32, copy=False)
+        Af = (Af / den[:, :, None]).astype(np.float32, copy=False)
         return self._r16(Af)
 
     def _conv_cf(self, A, Af, x_cl, W, H, round_in):
@@ -554,9 +554,9 @@ class Decoder:
         if self.fold_into_weights(R * OC4, N, IC, OC4):
             y4 = self._conv_cf(Ts, self._fold_A(Ts, s, den4), x_cl, W, H, self.f16)
         else:
-            xs = (x_cl * s[:, None, :]).astype(np.float32)
+            xs = (x_cl * s[:, None, :]).astype(np.float32, copy=False)
             y4 = self._conv_cf(Ts, Ts, xs, W, H, self.f16)
-            y4 = (y4 / den4[:, None, :]).astype(np.float32)
+            y4 = (y4 / den4[:, None, :]).astype(np.float32, copy=False)
         return subpix_lrelu_cl(y4, ab, W, H)
 
     def _styled_conv_cl(self, x_cl, W, H, base, s, den):
@@ -568,9 +568,9 @@ class Decoder:
         if self.fold_into_weights(R * OC, W * H, IC, OC):
             y = self._conv_cf(A, self._fold_A(A, s, den), x_cl, W, H, self.f16)
         else:
-            xs = (x_cl * s[:, None, :]).astype(np.float32)
+            xs = (x_cl * s[:, None, :]).astype(np.float32, copy=False)
             y = self._conv_cf(A, A, xs, W, H, self.f16)
-            y = (y / den[:, None, :]).astype(np.float32)
+            y = (y / den[:, None, :]).astype(np.float32, copy=False)
         return bias_lrelu(y, ab, 0)
 
     def _conv1(self, s0, d0):
@@ -578,7 +578,7 @@ class Decoder:
         C0 = self.ic[0]
         x = self.w["dec.input.input"].reshape(C0, 4, 4)
         Bb = s0.shape[0]
-        xs = (x[None] * s0[:, :, None, None]).astype(np.float32)   # (B, C0, 4, 4)
+        xs = (x[None] * s0[:, :, None, None]).astype(np.float32, copy=False)   # (B, C0, 4, 4)
         if self.isf16["dec.input.input"]:
             xs = round_f16(xs)  # F16 tensor result of ggml_mul
         W = self.w["dec.conv1.conv.weight"].reshape(C0, C0 * 9)      # row kw + 3kh + 9ic
@@ -590,7 +590,7 @@ class Decoder:
             for ox in range(4):
                 im[:, oy * 4 + ox, :] = pad[:, :, oy:oy + 3, ox:ox + 3].reshape(Bb, -1)
         y = mul_mat(W, self._r16(im) if self.f16 else im)              # (B, 16, C0)
-        y = (y / d0[:, None, :]).astype(np.float32)
+        y = (y / d0[:, None, :]).astype(np.float32, copy=False)
         return bias_lrelu(y, self.w["dec.conv1.activate.bias"], 0)
 
     def _fold_w4(self, W4, s, den):
@@ -598,9 +598,9 @@ class Decoder:
         (OC', IC, kh, kw), one frame: W * s[ic] / den[oc'] -> weight dtype."""
         Wf = _f32(W4)
         if s is not None:
-            Wf = (Wf * s[None, :, None, None]).astype(np.float32)
+            Wf = (Wf * s[None, :, None, None]).astype(np.float32, copy=False)
         if den is not None:
-            Wf = (Wf / den[:, None, None, None]).astype(np.float32)
+            Wf = (Wf / den[:, None, None, None]).astype(np.float32, copy=False)
         return Wf
 
     def _conv_sp(self, x_sp, Wt, round_in):
@@ -627,27 +627,27 @@ class Decoder:
         rbias = self.w[rb + ".bias"].reshape(3)
         lin = self.lin(r)
         # ToFlow: gemm_weight(fW, fstyle) then mul_mat (:1077-1085)
-        Af = (fW[None] * fs[:, None, :]).astype(np.float32)            # (B, 3, C)
+        Af = (fW[None] * fs[:, None, :]).astype(np.float32, copy=False)            # (B, 3, C)
         fl_cl = mul_mat(Af, out)                                        # (B, N, 3)
-        fl_cl = (fl_cl + fbias).astype(np.float32)
+        fl_cl = (fl_cl + fbias).astype(np.float32, copy=False)
         fl = np.ascontiguousarray(fl_cl.transpose(0, 2, 1).reshape(Bb, 3, r, r))
         if skf is not None:
-            fl = (fl + upfirdn2x(skf, self.w[fb + ".upsample.kernel"])).astype(np.float32)
-        gx = (tanh(fl[:, 0]) + lin[None, None, :]).astype(np.float32)
-        gy = (tanh(fl[:, 1]) + lin[None, :, None]).astype(np.float32)
+            fl = (fl + upfirdn2x(skf, self.w[fb + ".upsample.kernel"])).astype(np.float32, copy=False)
+        gx = (tanh(fl[:, 0]) + lin[None, None, :]).astype(np.float32, copy=False)
+        gy = (tanh(fl[:, 1]) + lin[None, :, None]).astype(np.float32, copy=False)
         m = sigmoid(fl[:, 2])                                           # (B, r, r)
         grid = np.stack([gx.reshape(-1), gy.reshape(-1)], axis=1)       # [2, N*B]
         sampled = bilinear_gather(self.feats[j], grid, r, r).reshape(Bb, N, C)
         m_row = m.reshape(Bb, N, 1)
-        warp = (sampled * m_row).astype(np.float32)
-        one_m = (np.float32(1.0) - m_row).astype(np.float32)
-        trunk = (warp + (out * one_m).astype(np.float32)).astype(np.float32)
+        warp = (sampled * m_row).astype(np.float32, copy=False)
+        one_m = (np.float32(1.0) - m_row).astype(np.float32, copy=False)
+        trunk = (warp + (out * one_m).astype(np.float32, copy=False)).astype(np.float32, copy=False)
         rgb_cl = mul_mat(rW, warp)                                      # (B, N, 3)
         rgb_cl = bias_lrelu(rgb_cl, rlb, 0)
-        rgb_cl = (rgb_cl + rbias).astype(np.float32)
+        rgb_cl = (rgb_cl + rbias).astype(np.float32, copy=False)
         rgb = np.ascontiguousarray(rgb_cl.transpose(0, 2, 1).reshape(Bb, 3, r, r))
         if sk is not None:
-            rgb = (rgb + upfirdn2x(sk, self.w[rb + ".upsample.kernel"])).astype(np.float32)
+            rgb = (rgb + upfirdn2x(sk, self.w[rb + ".upsample.kernel"])).astype(np.float32, copy=False)
         return fl, warp, trunk, rgb
 
     def decode_fast(self, latents, n_stages=None, want_taps=False):
@@ -705,11 +705,11 @@ class Decoder:
                     y = self._conv_sp(c1, W2f, self.f16)
                     out = bias_lrelu(y, self.w[b2 + ".activate.bias"], 2)
                     # ToFlow 1x1, weight-folded f32
-                    fWf = (fW * fs[c][None, :]).astype(np.float32)
+                    fWf = (fW * fs[c][None, :]).astype(np.float32, copy=False)
                     fl = mul_mat(fWf, np.ascontiguousarray(out.reshape(C, -1).T)).T.reshape(3, r, r)
-                    fl = (fl + fbias[:, None, None]).astype(np.float32)
+                    fl = (fl + fbias[:, None, None]).astype(np.float32, copy=False)
                     if skf is not None:
-                        fl = (fl + upfirdn2x(skf[c], fup)).astype(np.float32)
+                        fl = (fl + upfirdn2x(skf[c], fup)).astype(np.float32, copy=False)
                     sfn.append(fl)
                     xsg = np.stack([np.tile(lin, r), np.repeat(lin, r)])     # (2, N) planar
                     fg = flow_grid(fl, xsg)
@@ -721,9 +721,9 @@ class Decoder:
                     xn.append(trunk)
                     rgb = mul_mat(rW, np.ascontiguousarray(warp.reshape(C, -1).T)).T.reshape(3, r, r)
                     rgb = bias_lrelu(np.ascontiguousarray(rgb), rlb, 2)
-                    rgb = (rgb + rbias[:, None, None]).astype(np.float32)
+                    rgb = (rgb + rbias[:, None, None]).astype(np.float32, copy=False)
                     if sk is not None:
-                        rgb = (rgb + upfirdn2x(sk[c], rup)).astype(np.float32)
+                        rgb = (rgb + upfirdn2x(sk[c], rup)).astype(np.float32, copy=False)
                     skn.append(rgb)
                     if want_taps:
                         tc1.append(c1)

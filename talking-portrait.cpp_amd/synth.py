@@ -224,15 +224,59 @@ def image(seed=1005, res=512):
 
 # ---- flow-matching transformer (src/fmt.cpp, src/pipeline.cpp:12-91)
 
+class FmtConfig:
+    """fmt_model's hyper-parameters at their defaults (src/fmt.h:9-17), as
+    tpfm_default_config fills them; keyword arguments override"""
+
+    def __init__(self, **kw):
+        self.dim_h, self.depth, self.n_heads = 1024, 8, 8
+        self.dim_w, self.dim_a, self.dim_e = 512, 512, 7
+        self.chunk_frames, self.prev_frames = 50, 10
+        self.attn_window, self.t_freq_dim, self.nfe = 2, 256, 10
+        self.mlp_ratio, self.ln_eps = 4.0, 1e-6
+        self.a_cfg, self.e_cfg, self.r_cfg = 2.0, 1.0, 1.0
+        for k, v in kw.items():
+            if not hasattr(self, k):
+                raise AttributeError(k)
+            setattr(self, k, v)
+        self.total = self.chunk_frames + self.prev_frames
+
+    @property
+    def dim_c(self):
+        return self.dim_w + self.dim_a + self.dim_e
+
+    @property
+    def dim_mlp(self):
+        return int(self.dim_h * self.mlp_ratio)
+
+
+def fmt_tensor_shapes(cfg):
+    """(name, torch shape) of every FMT tensor in GGUF names
+    (src/fmt.cpp:61-150); cfg: any object with FmtConfig's attributes"""
+    H = cfg.dim_h
+    v = [("t_embedder.mlp.0.weight", (H, cfg.t_freq_dim)), ("t_embedder.mlp.0.bias", (H,)),
+         ("t_embedder.mlp.2.weight", (H, H)), ("t_embedder.mlp.2.bias", (H,)),
+         ("c_embedder.weight", (H, cfg.dim_c)), ("c_embedder.bias", (H,)),
+         ("x_embedder.proj.weight", (H, cfg.dim_w)), ("x_embedder.proj.bias", (H,)),
+         ("pos_embed", (1, cfg.total, H))]
+    for i in range(cfg.depth):
+        b = f"blocks.{i}"
+        for part, rows, cols in (("adaLN_modulation.1", 6 * H, H), ("attn.qkv", 3 * H, H), ("attn.proj", H, H),
+                                 ("mlp.fc1", cfg.dim_mlp, H), ("mlp.fc2", H, cfg.dim_mlp)):
+            v += [(f"{b}.{part}.weight", (rows, cols)), (f"{b}.{part}.bias", (rows,))]
+    v += [("decoder.adaLN_modulation.1.weight", (2 * H, H)), ("decoder.adaLN_modulation.1.bias", (2 * H,)),
+          ("decoder.linear.weight", (cfg.dim_w, H)), ("decoder.linear.bias", (cfg.dim_w,))]
+    return v
+
+
 def fmt_raw_weights(cfg, seed=1006, ftype="f32"):
     """name -> (float32 array in torch shape, f16_in_file) for an FMT of
-    config `cfg` (oracle.fmt.Config), seed 1006: Linear weights
-    ~ N(0,1)/sqrt(fan_in) (adaLN weights x0.5, so the gates and shifts are
-    O(0.1-1) instead of the adaLN-Zero start), biases ~ N(0,1) * 0.02,
-    pos_embed ~ N(0,1) * 0.1."""
-    from oracle import fmt as OF
+    config `cfg` (FmtConfig or any object with its attributes), seed 1006:
+    Linear weights ~ N(0,1)/sqrt(fan_in) (adaLN weights x0.5, so the gates
+    and shifts are O(0.1-1) instead of the adaLN-Zero start), biases
+    ~ N(0,1) * 0.02, pos_embed ~ N(0,1) * 0.1."""
     out = {}
-    for name, shape in OF.weight_names(cfg):
+    for name, shape in fmt_tensor_shapes(cfg):
         g = _rng(seed, name)
         a = g.standard_normal(shape, dtype=np.float32)
         if name.endswith(".weight"):

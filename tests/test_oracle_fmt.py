@@ -67,3 +67,12 @@ def test_sampler_is_euler_with_cfg(oracle_fmt):
     v = F.forward(np.concatenate([io["prev_x"], io["x0"]]), cond, 0.0)
     vc = (v[0] + 2.0 * (v[2] - v[0])) + 1.0 * (v[1] - v[2])
     assert np.allclose(x, io["x0"] + vc[2:], rtol=1e-5, atol=1e-5)
+
+
+def test_tensor_list_matches_synth(oracle_fmt):
+    """the oracle's FMT tensor inventory and the synthetic-weight generator's
+    (two independent restatements of src/fmt.cpp:61-150) agree"""
+    for kw in ({}, dict(dim_h=128, depth=2, n_heads=4, dim_w=64, dim_a=64)):
+        cfg = oracle_fmt.Config(**kw)
+        assert oracle_fmt.weight_names(cfg) == synth.fmt_tensor_shapes(cfg)
+        assert oracle_fmt.weight_names(cfg) == synth.fmt_tensor_shapes(synth.FmtConfig(**kw))
