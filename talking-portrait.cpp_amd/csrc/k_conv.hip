@@ -307,7 +307,7 @@ int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int
         return A_ORDER_FRAG;
     if (mode == MODE_DENSE && H == W && f16 && OC == 256 && IC % 32 == 0 && modconv_fusable(OC, H, f16))
         return A_ORDER_RING_TAP;
-    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_RING;
+    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return modconv_hring_frag_a ? A_ORDER_FRAG : A_ORDER_RING;
     return A_ORDER_TAP;
 }
 

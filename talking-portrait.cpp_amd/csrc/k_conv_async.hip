@@ -651,6 +651,179 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
     });
 }
 
+// ---------------------------------------------------------------------------
+// The halo ring with A read by every wave straight from L2 in MFMA fragment
+// order (A_ORDER_FRAG: each fragment is one contiguous 1 KB) instead of
+// through an LDS ring.  Waves are 4 x 2 with 64 x 128 tiles, so a wave reads
+// 2 A fragments and 4 B fragments per 16-wide k step.  The two waves that
+// share A rows read the same lines, and the second finds them in L1.  The LDS
+// holds only the two halo buffers, so the one barrier per 32-channel chunk
+// (9 k tiles) is the halo hand-over; A needs no barrier.
+//   * A fragments are requested two k tiles ahead into three register sets
+//     (k tile t in set t % 3; 9 taps per chunk keep the set of a tap fixed);
+//   * the B fragments of the next k step are read from LDS while the
+//     current step's MFMAs run;
+//   * the halo of chunk c+1 is requested as chunk c starts; at the end of
+//     chunk c a wave waits until at most the A loads of the next two k tiles
+//     (issued after that halo) are outstanding, then barriers.
+// The k order (chunk, tap, 16-wide step) is the hring kernel's, so the sums
+// are the same bits.
+template <int MODE>
+__global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int tiles_x, int tiles_frame) {
+    typedef half_t TA;
+    constexpr int NW = 8, NT = NW * 64, WN = 2;
+    constexpr int BM = 256, BN = HR_TH * HR_TW;
+    constexpr int TM = 2, TN = 4;                        // 64 x 128 per wave
+    constexpr int LPH = HR_HBUF / 1024 / NW;             // halo DMA instructions per wave per chunk
+    constexpr int ORS = BM * 2 + 16, OUT = BN * ORS;     // staged f16 output, one padded row per pixel
+    constexpr int LDS = 2 * HR_HBUF > OUT ? 2 * HR_HBUF : OUT;
+    constexpr int A_PER_TILE = 2 * TM;                   // A loads per wave per k tile
+    static_assert(BM / 32 == 4 * TM && BN / 32 == WN * TN, "wave grid");
+    __shared__ __attribute__((aligned(16))) char smem[LDS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WN, wn = wid % WN;
+    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
+    const int mt = tile % p.MT, nt = tile / p.MT;
+    const int fr = nt / tiles_frame;
+    const int trem = nt - fr * tiles_frame;
+    const int ty = trem / tiles_x;
+    const int y0 = ty * HR_TH, x0 = (trem - ty * tiles_x) * HR_TW;
+    const int m0 = mt * BM;
+    const int IC = p.IC, H = p.H, W = p.W;
+    const int NC = IC / 32, KSA = IC / 16, MB = p.M / 32;
+
+    // A fragment (tap, ks) of row block w = m0/32 + wm*TM + a: 1 KB at
+    // ((tap*KSA + ks)*MB + w) KB; this lane's 16 bytes of it
+    const TA *abase = (const TA *) p.A + ((int64_t) (m0 / 32 + wm * TM)) * 512 + lane * 8;
+    auto afrag = [&](int tap, int ks, int a) -> u32x4 {
+        return *(const u32x4 *) (abase + ((int64_t) (tap * KSA + ks) * MB + a) * 512);
+    };
+    u32x4 af[3][TM][2];
+    auto load_a = [&](int c, int tap, u32x4 (&dst)[TM][2]) {
+        static_for<2>([&](auto s) { static_for<TM>([&](auto a) { dst[a][s] = afrag(tap, 2 * c + s, a); }); });
+    };
+
+    // halo DMA, as modconv3x3_hring_kernel
+    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
+    const TA *hsrc[LPH];
+    bool hok[LPH];
+#pragma unroll
+    for (int h = 0; h < LPH; h++) {
+        const int u = (wid * LPH + h) * 64 + lane;
+        const int hp = u / 5, q = u - hp * 5;
+        const int hy = hp / HR_HWD, hx = hp - hy * HR_HWD;
+        const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
+        hok[h] = q < 4 && hp < HR_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
+        hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * IC + q * 8 : Xf;
+    }
+    const void *zero = (const void *) g_zero16;
+    auto issue_h = [&](int c) {
+        char *buf = smem + (c & 1) * HR_HBUF;
+        static_for<LPH>([&](auto h) {
+            const void *g = hok[h] ? (const void *) (hsrc[h] + c * 32) : zero;
+            __builtin_amdgcn_global_load_lds(g, TPMD_LDS(buf + (wid * LPH + h) * 1024), 16, 0, 0);
+        });
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; a++)
+#pragma unroll
+        for (int b = 0; b < TN; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+
+    const int lrow = lane & 31, khalf = lane >> 5;
+    // this lane's halo pixel for tap (0, 0) of fragment b: block row TN*wn + b, column lrow
+    const int hbase = ((TN * wn) * HR_HWD + lrow) * HR_PXB + khalf * 16;
+    auto read_b = [&](const char *hb, int tap, int s, u32x4 (&bf)[TN]) {
+        const int dy = tap / 3, dx = tap - dy * 3;
+        const char *q = hb + (dy * HR_HWD + dx) * HR_PXB + s * 32;
+        static_for<TN>([&](auto b) { bf[b] = *(const u32x4 *) (q + b * HR_HWD * HR_PXB); });
+    };
+
+    issue_h(0);
+    load_a(0, 0, af[0]);
+    load_a(0, 1, af[1]);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * A_PER_TILE));   // the halo (issued first) has landed
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    for (int c = 0; c < NC; c++) {
+        const char *hb = smem + hbase + (c & 1) * HR_HBUF;
+        if (c + 1 < NC) issue_h(c + 1);   // its buffer's last reads (chunk c-1) ended before the barrier
+        u32x4 bcur[TN];
+        read_b(hb, 0, 0, bcur);
+        static_for<18>([&](auto q) {
+            constexpr int u = q / 2, s = q % 2;
+            if constexpr (s == 0) {
+                // A of k tile t + 2 (tap u + 2 of this chunk, or of the next)
+                if constexpr (u + 2 < 9) load_a(c, u + 2, af[(u + 2) % 3]);
+                else if (c + 1 < NC) load_a(c + 1, u + 2 - 9, af[(u + 2) % 3]);
+            }
+            u32x4 bnext[TN];
+            if constexpr (q + 1 < 18) read_b(hb, (q + 1) / 2, (q + 1) % 2, bnext);
+            static_for<TM>([&](auto a) {
+                static_for<TN>([&](auto b) { mfma_op<TA>::run(af[u % 3][a][s], bcur[b], acc[a][b]); });
+            });
+            if constexpr (q + 1 < 18) static_for<TN>([&](auto b) { bcur[b] = bnext[b]; });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        if (c + 1 < NC) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * A_PER_TILE));   // halo c+1 landed
+            __builtin_amdgcn_s_barrier();   // every wave's part of it; chunk c's reads done
+            asm volatile("" ::: "memory");
+        }
+    }
+
+    // f16 store epilogue through LDS, as modconv3x3_hring_kernel
+    __syncthreads();
+    static_for<TN>([&](auto b) {
+        const int nl = (wn * TN + b) * 32 + lrow;
+        static_for<TM>([&](auto a) {
+            static_for<4>([&](auto i) {
+                const int ml = (wm * TM + a) * 32 + i * 8 + khalf * 4;
+                const int m = m0 + ml;
+                const int o = MODE == MODE_DENSE ? m : m % p.OC;
+                const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + o);
+                const floatx4 bb = *(const floatx4 *) (p.bias + o);
+                floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
+                if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
+                half4 hv;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float v = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                    if (p.out_scale) v *= sc[j];
+                    hv[j] = (half_t) v;
+                }
+                *(half4 *) (smem + nl * ORS + ml * 2) = hv;
+            });
+        });
+    });
+    __syncthreads();
+    constexpr int CPR = BM / 8, NCH = BN * CPR, STEP = NT / CPR;
+    static_assert(NCH % NT == 0 && NT % CPR == 0 && HR_TW % STEP == 0, "store pass");
+    const int mc = tid % CPR;
+    const int m = m0 + mc * 8;
+    int cls = 0, o = m;
+    if constexpr (MODE == MODE_SUBPIX) {
+        cls = m / p.OC;
+        o = m - cls * p.OC;
+    }
+    const int64_t HW = (int64_t) H * W;
+    half_t *Yp = (half_t *) p.Y;
+    static_for<NCH / NT>([&](auto j) {
+        const int nl = tid / CPR + j * STEP;
+        const int y = y0 + nl / HR_TW, x = x0 + nl % HR_TW;
+        int64_t opix;
+        if constexpr (MODE == MODE_DENSE) opix = fr * HW + (int64_t) y * W + x;
+        else opix = fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
+        const u32x4 v = *(const u32x4 *) (smem + nl * ORS + mc * 16);
+        *(u32x4 *) (Yp + opix * p.OC + o) = v;
+    });
+}
+
 // the 256-row halo ring: f16 operands and output, M a multiple of 256, input
 // maps of 8 x 32 blocks, and enough tiles at 16 frames to give every CU one
 bool modconv_hring_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
@@ -671,6 +844,15 @@ hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st) {
     p.T = 9 * p.IC / 32;
     const int tiles_x = p.W / HR_TW, tiles_frame = tiles_x * (p.H / HR_TH);
     const int64_t tiles = (int64_t) p.MT * (p.N / HW) * tiles_frame;
+    if (modconv_hring_frag_a) {
+        if (mode == MODE_DENSE)
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE>), dim3((unsigned) tiles), dim3(512), 0, st, p,
+                               tiles_x, tiles_frame);
+        else
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX>), dim3((unsigned) tiles), dim3(512), 0, st, p,
+                               tiles_x, tiles_frame);
+        return hipGetLastError();
+    }
     if (mode == MODE_DENSE)
         hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_DENSE, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0, st,
                            p, tiles_x, tiles_frame);

@@ -123,6 +123,10 @@ bool modconv_tail_async_ok(int OC, int r);
 // 256-row tiles over 8 x 32 pixel blocks with the input halo in LDS
 // (k_conv_async.hip); A in chunk-major order [M][IC/32][9][32]
 bool modconv_hring_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
+// the halo-ring convs read A straight from L2 in fragment order
+// (modconv3x3_hfrag_kernel, A_ORDER_FRAG) rather than through an LDS ring
+// (modconv3x3_hring_kernel, A_ORDER_RING)
+constexpr bool modconv_hring_frag_a = true;
 hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st);
 // k_conv_up.hip: f16 composed sub-pixel up-conv 64 -> 32 channels with f16
 // output, on 4 x 32 halo tiles (H % 4 == 0, W % 32 == 0)
