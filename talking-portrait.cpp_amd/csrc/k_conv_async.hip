@@ -663,12 +663,11 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
 //     (k tile t in set t % 3; 9 taps per chunk keep the set of a tap fixed);
 //   * the B fragments of the next k step are read from LDS while the
 //     current step's MFMAs run;
-//   * the halo of chunk c+1 is requested as chunk c starts; at the end of
-//     chunk c a wave waits until at most the A loads of the next two k tiles
-//     (issued after that halo) are outstanding, then barriers.
+//   * the halo of chunk c+1 is loaded into registers early in chunk c and
+//     written to the other LDS buffer late in it; one barrier ends the chunk.
 // The k order (chunk, tap, 16-wide step) is the hring kernel's, so the sums
 // are the same bits.
-template <int MODE>
+template <int MODE, int NC>
 __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int tiles_x, int tiles_frame) {
     typedef half_t TA;
     constexpr int NW = 8, NT = NW * 64, WN = 2;
@@ -691,8 +690,9 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     const int ty = trem / tiles_x;
     const int y0 = ty * HR_TH, x0 = (trem - ty * tiles_x) * HR_TW;
     const int m0 = mt * BM;
-    const int IC = p.IC, H = p.H, W = p.W;
-    const int NC = IC / 32, KSA = IC / 16, MB = p.M / 32;
+    constexpr int IC = NC * 32, KSA = IC / 16;
+    const int H = p.H, W = p.W;
+    const int MB = p.M / 32;
 
     // A fragment (tap, ks) of row block w = m0/32 + wm*TM + a: 1 KB at
     // ((tap*KSA + ks)*MB + w) KB; this lane's 16 bytes of it
@@ -718,13 +718,17 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
         hok[h] = q < 4 && hp < HR_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
         hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * IC + q * 8 : Xf;
     }
-    const void *zero = (const void *) g_zero16;
-    auto issue_h = [&](int c) {
+    // the halo goes through registers rather than the LDS DMA path: the
+    // compiler then counts every load exactly, while after an LDS DMA it
+    // waits for all loads in flight before the next MFMA
+    const u32x4 *zero = (const u32x4 *) g_zero16;
+    u32x4 hreg[LPH];
+    auto load_h = [&](int c) {
+        static_for<LPH>([&](auto h) { hreg[h] = *(hok[h] ? (const u32x4 *) (hsrc[h] + c * 32) : zero); });
+    };
+    auto store_h = [&](int c) {
         char *buf = smem + (c & 1) * HR_HBUF;
-        static_for<LPH>([&](auto h) {
-            const void *g = hok[h] ? (const void *) (hsrc[h] + c * 32) : zero;
-            __builtin_amdgcn_global_load_lds(g, TPMD_LDS(buf + (wid * LPH + h) * 1024), 16, 0, 0);
-        });
+        static_for<LPH>([&](auto h) { *(u32x4 *) (buf + (wid * LPH + h) * 1024 + lane * 16) = hreg[h]; });
     };
 
     floatx16 acc[TM][TN];
@@ -744,38 +748,41 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
         static_for<TN>([&](auto b) { bf[b] = *(const u32x4 *) (q + b * HR_HWD * HR_PXB); });
     };
 
-    issue_h(0);
+    load_h(0);
     load_a(0, 0, af[0]);
     load_a(0, 1, af[1]);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * A_PER_TILE));   // the halo (issued first) has landed
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    for (int c = 0; c < NC; c++) {
+    store_h(0);
+    __syncthreads();
+    // the chunks unrolled (NC is a template argument), so the compiler's
+    // memory-counter waits are exact: no wait drains the loads in flight
+    static_for<NC>([&](auto cc) {
+        constexpr int c = decltype(cc)::value;
         const char *hb = smem + hbase + (c & 1) * HR_HBUF;
-        if (c + 1 < NC) issue_h(c + 1);   // its buffer's last reads (chunk c-1) ended before the barrier
         u32x4 bcur[TN];
         read_b(hb, 0, 0, bcur);
         static_for<18>([&](auto q) {
             constexpr int u = q / 2, s = q % 2;
+            // requests first (A of k tile t + 2, B of the next step), then the MFMAs
             if constexpr (s == 0) {
-                // A of k tile t + 2 (tap u + 2 of this chunk, or of the next)
                 if constexpr (u + 2 < 9) load_a(c, u + 2, af[(u + 2) % 3]);
-                else if (c + 1 < NC) load_a(c + 1, u + 2 - 9, af[(u + 2) % 3]);
+                else if constexpr (c + 1 < NC) load_a(c + 1, u + 2 - 9, af[(u + 2) % 3]);
             }
             u32x4 bnext[TN];
             if constexpr (q + 1 < 18) read_b(hb, (q + 1) / 2, (q + 1) % 2, bnext);
+            __builtin_amdgcn_sched_barrier(0);
             static_for<TM>([&](auto a) {
                 static_for<TN>([&](auto b) { mfma_op<TA>::run(af[u % 3][a][s], bcur[b], acc[a][b]); });
             });
             if constexpr (q + 1 < 18) static_for<TN>([&](auto b) { bcur[b] = bnext[b]; });
             __builtin_amdgcn_sched_barrier(0);
+            // the next chunk's halo: requested after the first step, written
+            // (into the buffer whose last reads, chunk c-1's, ended before
+            // the barrier) after the 13th, when it has long arrived
+            if constexpr (q == 0 && c + 1 < NC) load_h(c + 1);
+            if constexpr (q == 12 && c + 1 < NC) store_h(c + 1);
         });
-        if (c + 1 < NC) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * A_PER_TILE));   // halo c+1 landed
-            __builtin_amdgcn_s_barrier();   // every wave's part of it; chunk c's reads done
-            asm volatile("" ::: "memory");
-        }
-    }
+        if constexpr (c + 1 < NC) __syncthreads();   // halo c+1 written, chunk c's reads done
+    });
 
     // f16 store epilogue through LDS, as modconv3x3_hring_kernel
     __syncthreads();
@@ -829,6 +836,7 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
 bool modconv_hring_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
     const int M = mode == MODE_DENSE ? OC : 4 * OC;
     if (!f16 || !out_f16 || IC % 32 != 0 || M % 256 != 0 || H % HR_TH != 0 || W % HR_TW != 0) return false;
+    if (modconv_hring_frag_a && IC != 32 && IC != 64 && IC != 128 && IC != 256 && IC != 512) return false;
     return (int64_t) (M / 256) * 16 * (H / HR_TH) * (W / HR_TW) >= 256;
 }
 
@@ -845,13 +853,24 @@ hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st) {
     const int tiles_x = p.W / HR_TW, tiles_frame = tiles_x * (p.H / HR_TH);
     const int64_t tiles = (int64_t) p.MT * (p.N / HW) * tiles_frame;
     if (modconv_hring_frag_a) {
-        if (mode == MODE_DENSE)
-            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE>), dim3((unsigned) tiles), dim3(512), 0, st, p,
-                               tiles_x, tiles_frame);
-        else
-            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX>), dim3((unsigned) tiles), dim3(512), 0, st, p,
-                               tiles_x, tiles_frame);
-        return hipGetLastError();
+        auto go = [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            if (mode == MODE_DENSE)
+                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC>), dim3((unsigned) tiles), dim3(512), 0,
+                                   st, p, tiles_x, tiles_frame);
+            else
+                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC>), dim3((unsigned) tiles), dim3(512), 0,
+                                   st, p, tiles_x, tiles_frame);
+            return hipGetLastError();
+        };
+        switch (p.IC) {
+            case 32: return go(std::integral_constant<int, 1>{});
+            case 64: return go(std::integral_constant<int, 2>{});
+            case 128: return go(std::integral_constant<int, 4>{});
+            case 256: return go(std::integral_constant<int, 8>{});
+            case 512: return go(std::integral_constant<int, 16>{});
+            default: return hipErrorInvalidValue;
+        }
     }
     if (mode == MODE_DENSE)
         hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_DENSE, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0, st,
