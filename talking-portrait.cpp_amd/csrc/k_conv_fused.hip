@@ -201,12 +201,13 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
 
 // ---------------------------------------------------------------------------
 // The 64-channel stage (IC = OC = 64): 4 x 32 blocks (the tail's 128 pixels).
-// The halo goes to LDS through registers as above; the 64 x 576 weight
-// matrix is too large to keep, so it streams through a 2-stage LDS ring by
-// the DMA path, one tap (8 fragments of 1 KB) at a time, shared by the four
-// waves; wave w computes weight rows 32*(w&1) .. +31 for block rows
-// 2*(w>>1) .. +1.  FRAG: A in fragment order (A_ORDER_FRAG), contiguous
-// 1 KB per fragment DMA.
+// The halo goes to LDS through registers as above.  Wave w computes weight
+// rows 32*(w&1) .. +31 for block rows 2*(w>>1) .. +1, and reads its A
+// fragments (4 of 1 KB per tap) straight from L2 into registers, two taps
+// ahead of the MFMAs: no LDS for A and no barrier inside the conv, so the
+// taps do not wait on one another's memory round trips.  The workgroup's LDS
+// (halo, then the activated tile) is 40 KB: four workgroups per CU.  FRAG: A
+// in fragment order (A_ORDER_FRAG), each fragment one contiguous 1 KB.
 struct fused64_cfg {
     static constexpr int C = 64, NT = 256, TH = 4, TW = 32, BN = TH * TW;
     static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
@@ -219,13 +220,10 @@ struct fused64_cfg {
     static constexpr int RPW = 2;                       // block rows per wave
     typedef tile_tail_lds<C, BN> L;
     static constexpr int HALO = HPX * PXB;
-    static constexpr int AOFF = (HALO + 255) / 256 * 256;
-    static constexpr int ASTG = FPT * 1024;             // one tap of A
-    static constexpr int CONV = AOFF + 2 * ASTG;
+    static constexpr int CONV = (HALO + 255) / 256 * 256;
     static constexpr int TAIL = L::WFS0 * 4;
     static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
-    static_assert(FPT % (NT / 64) == 0, "A fragments per wave");
 };
 
 // s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt not waited on
@@ -240,7 +238,6 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
     constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
     constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, FPT = F::FPT, RPW = F::RPW;
     constexpr int K = 9 * C;
-    constexpr int APW = FPT / (NT / 64);                // A fragment DMAs per wave per tap
     __shared__ __attribute__((aligned(16))) char smem[F::LDS];
     float *so = (float *) smem, *prm = so + L::PRM0, *wfs = (float *) (smem + F::WFS);
 
@@ -256,17 +253,16 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
     const int y0 = ty * F::TH, x0 = tx * TW;
     const int n0 = (fr * H + y0) * W + x0;
 
-    // A fragment f of tap t (f = step*2 + row block): lane l holds
-    // A[32*(f&1) + l%32][t*64 + (f>>1)*16 + (l/32)*8 .. +8]
+    // A fragment (tap t, step s) of this wave's row block mb: lane l holds
+    // A[32*mb + l%32][t*64 + s*16 + (l/32)*8 .. +8]; tap t's fragments go to
+    // register set t % 3
     const TA *Ab = (const TA *) p.A;
-    auto issue_a = [&](int t) {
-        char *stage = smem + F::AOFF + (t & 1) * F::ASTG;
-        static_for<APW>([&](auto j) {
-            const int f = wid * APW + j;
-            const TA *src = FRAG ? Ab + (t * FPT + f) * 512 + lane * 8
-                                 : Ab + (int64_t) ((f & 1) * 32 + lrow) * K + t * C + (f >> 1) * 16 + khalf * 8;
-            __builtin_amdgcn_global_load_lds((const void *) src,
-                                             (__attribute__((address_space(3))) void *) (stage + f * 1024), 16, 0, 0);
+    const TA *arow = FRAG ? Ab + (mb * 64 + lane) * 8 : Ab + (int64_t) (mb * 32 + lrow) * K + khalf * 8;
+    u32x4 af[3][KS];
+    auto load_a = [&](int t, u32x4 (&dst)[KS]) {
+        static_for<KS>([&](auto st) {
+            constexpr int s = decltype(st)::value;
+            dst[s] = *(const u32x4 *) (arow + (FRAG ? (t * FPT + s * 2) * 512 : t * C + s * 16));
         });
     };
 
@@ -286,8 +282,8 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
             }
         });
     });
-    issue_a(0);
-    issue_a(1);
+    load_a(0, af[0]);
+    load_a(1, af[1]);
     const tail_wfs_regs<C, NT> wr = tile_tail_wfs_load<C, NT>(ta, fr, tid);
     static_for<PF>([&](auto i) {
         const int ch = tid + i * NT;
@@ -297,36 +293,28 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
         }
     });
     tile_tail_wfs_store<C, NT>(wfs, tid, wr);
-    __builtin_amdgcn_s_waitcnt(fused_waitcnt_vm(0));
-    __syncthreads();  // halo, wfs and both A stages in place
+    __syncthreads();  // halo and wfs in place
 
     floatx16 acc[RPW];
     static_for<RPW>([&](auto b) {
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[b][v] = 0.0f;
     });
-    static_for<9>([&](auto tap) {
+    static_for<9>([&](auto tp) {
+        constexpr int tap = decltype(tp)::value;
         constexpr int dy = tap / 3, dx = tap % 3;
-        if constexpr (tap > 0) {
-            // this wave's part of tap `tap` (its only DMAs in flight) landed ...
-            __builtin_amdgcn_s_waitcnt(fused_waitcnt_vm(0));
-            __builtin_amdgcn_s_barrier();  // ... every wave's part, and tap-1's stage is free
-            asm volatile("" ::: "memory");
-            if constexpr (tap + 1 < 9) issue_a(tap + 1);
-        }
-        const char *ast = smem + F::AOFF + (tap & 1) * F::ASTG;
+        if constexpr (tap + 2 < 9) load_a(tap + 2, af[(tap + 2) % 3]);
         static_for<KS>([&](auto s) {
-            const u32x4 af = *(const u32x4 *) (ast + (s * 2 + mb) * 1024 + lane * 16);
             static_for<RPW>([&](auto b) {
                 const int hrow = rg * RPW + b + dy;
                 const u32x4 bf =
                     *(const u32x4 *) (smem + (hrow * HWD + lrow + dx) * PXB + (s * 2 + khalf) * 16);
-                mfma_op<TA>::run(af, bf, acc[b]);
+                mfma_op<TA>::run(af[tap % 3][s], bf, acc[b]);
             });
         });
         __builtin_amdgcn_sched_barrier(0);
     });
-    __syncthreads();  // halo and A reads done: the LDS becomes the activated tile
+    __syncthreads();  // halo reads done: the LDS becomes the activated tile
 
     // accumulator (b, v): channel mb*32 + (v/4)*8 + (lane/32)*4 + v%4, tile pixel (rg*2 + b)*32 + lane%32
     static_for<RPW>([&](auto b) {
