@@ -200,50 +200,55 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
 }
 
 // ---------------------------------------------------------------------------
-// The 64-channel stage (IC = OC = 64): 4 x 32 blocks (the tail's 128 pixels).
-// The halo goes to LDS through registers as above.  Wave w computes weight
-// rows 32*(w&1) .. +31 for block rows 2*(w>>1) .. +1, and reads its A
-// fragments (4 of 1 KB per tap) straight from L2 into registers, two taps
-// ahead of the MFMAs: no LDS for A and no barrier inside the conv, so the
-// taps do not wait on one another's memory round trips.  The workgroup's LDS
-// (halo, then the activated tile) is 40 KB: four workgroups per CU.  FRAG: A
+// The 64- and 128-channel stages (IC = OC = C): 4 x 32 blocks (the tail's 128
+// pixels), four waves.  The halo goes to LDS through registers as above.  The
+// C/32 row blocks of 32 weight rows are split over the waves: C = 64, wave w
+// computes row block w&1 for block rows 2*(w>>1) .. +1; C = 128, row block w
+// for all four block rows.  Every wave reads its A fragments (C/16 of 1 KB
+// per tap) straight from L2 into registers, two taps ahead of the MFMAs: no
+// LDS for A and no barrier inside the conv, so the taps do not wait on one
+// another's memory round trips.  LDS: the halo, then the activated tile
+// (40 KB at C = 64: four workgroups per CU; 73 KB at C = 128: two).  FRAG: A
 // in fragment order (A_ORDER_FRAG), each fragment one contiguous 1 KB.
-struct fused64_cfg {
-    static constexpr int C = 64, NT = 256, TH = 4, TW = 32, BN = TH * TW;
+template <int C_>
+struct fusedh_cfg {
+    static constexpr int C = C_, NT = 256, TH = 4, TW = 32, BN = TH * TW;
     static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
     static constexpr int PXB = C * 2 + 16;
     static constexpr int CPP = C * 2 / 16;
     static constexpr int HCH = HPX * CPP;
     static constexpr int PF = (HCH + NT - 1) / NT;
     static constexpr int KS = C / 16;                   // MFMA k steps per tap
-    static constexpr int FPT = 2 * KS;                  // A fragments per tap (2 row blocks)
-    static constexpr int RPW = 2;                       // block rows per wave
+    static constexpr int MBK = C / 32;                  // 32-row blocks of A
+    static constexpr int RG = (NT / 64) / MBK;          // wave groups along the block rows
+    static constexpr int RPW = TH / RG;                 // block rows per wave
     typedef tile_tail_lds<C, BN> L;
     static constexpr int HALO = HPX * PXB;
     static constexpr int CONV = (HALO + 255) / 256 * 256;
     static constexpr int TAIL = L::WFS0 * 4;
     static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
+    static_assert(RG * MBK == NT / 64 && RG * RPW == TH, "wave grid");
 };
 
 // s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt not waited on
 constexpr int fused_waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
 
-template <typename TF, typename TT, bool FRAG>
-__global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
-                                                          int tiles_frame) {
+template <typename TF, typename TT, int C_, bool FRAG>
+__global__ __launch_bounds__(256) void convh_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
+                                                         int tiles_frame) {
     typedef half_t TA;
-    typedef fused64_cfg F;
+    typedef fusedh_cfg<C_> F;
     typedef typename F::L L;
     constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
-    constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, FPT = F::FPT, RPW = F::RPW;
+    constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, MBK = F::MBK, RPW = F::RPW;
     constexpr int K = 9 * C;
     __shared__ __attribute__((aligned(16))) char smem[F::LDS];
     float *so = (float *) smem, *prm = so + L::PRM0, *wfs = (float *) (smem + F::WFS);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wid = tid >> 6;
-    const int mb = wid & 1, rg = wid >> 1;
+    const int mb = wid % MBK, rg = wid / MBK;
     const int lrow = lane & 31, khalf = lane >> 5;
     const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
     const int fr = tile / tiles_frame;
@@ -254,15 +259,15 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
     const int n0 = (fr * H + y0) * W + x0;
 
     // A fragment (tap t, step s) of this wave's row block mb: lane l holds
-    // A[32*mb + l%32][t*64 + s*16 + (l/32)*8 .. +8]; tap t's fragments go to
-    // register set t % 3
+    // A[32*mb + l%32][t*C + s*16 + (l/32)*8 .. +8] (fragment order: fragment
+    // (t*KS + s)*MBK + mb); tap t's fragments go to register set t % 3
     const TA *Ab = (const TA *) p.A;
     const TA *arow = FRAG ? Ab + (mb * 64 + lane) * 8 : Ab + (int64_t) (mb * 32 + lrow) * K + khalf * 8;
     u32x4 af[3][KS];
     auto load_a = [&](int t, u32x4 (&dst)[KS]) {
         static_for<KS>([&](auto st) {
             constexpr int s = decltype(st)::value;
-            dst[s] = *(const u32x4 *) (arow + (FRAG ? (t * FPT + s * 2) * 512 : t * C + s * 16));
+            dst[s] = *(const u32x4 *) (arow + (FRAG ? (t * KS + s) * MBK * 512 : t * C + s * 16));
         });
     };
 
@@ -333,25 +338,34 @@ __global__ __launch_bounds__(256) void conv64_tail_kernel(ConvParams p, TailArgs
     tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
 }
 
-bool modconv_fused64_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 64 && OC == 64 && r % 32 == 0; }
+bool modconv_fused64_ok(bool f16, int IC, int OC, int r) {
+    return f16 && IC == OC && (OC == 64 || OC == 128) && r % 32 == 0;
+}
 
 hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
                                   hipStream_t st) {
-    if (p.IC != 64 || p.OC != 64 || p.M != 64 || p.W % 32 != 0 || p.H % fused64_cfg::TH != 0)
+    constexpr int TH = fusedh_cfg<64>::TH;
+    if (p.IC != p.OC || (p.OC != 64 && p.OC != 128) || p.M != p.OC || p.W % 32 != 0 || p.H % TH != 0)
         return hipErrorInvalidValue;
-    const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / fused64_cfg::TH);
+    const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
-#define TPMD_L(TT, FR) \
-    hipLaunchKernelGGL((conv64_tail_kernel<half_t, TT, FR>), grid, dim3(256), 0, st, p, ta, tiles_x, tiles_frame)
-    if (trunk_f16) {
-        if (frag) TPMD_L(half_t, true);
-        else TPMD_L(half_t, false);
-    } else {
-        if (frag) TPMD_L(float, true);
-        else TPMD_L(float, false);
-    }
+    auto go = [&](auto c) {
+        constexpr int C = decltype(c)::value;
+#define TPMD_L(TT, FR)                                                                                       \
+    hipLaunchKernelGGL((convh_tail_kernel<half_t, TT, C, FR>), grid, dim3(256), 0, st, p, ta, tiles_x, \
+                       tiles_frame)
+        if (trunk_f16) {
+            if (frag) TPMD_L(half_t, true);
+            else TPMD_L(half_t, false);
+        } else {
+            if (frag) TPMD_L(float, true);
+            else TPMD_L(float, false);
+        }
 #undef TPMD_L
+    };
+    if (p.OC == 64) go(std::integral_constant<int, 64>{});
+    else go(std::integral_constant<int, 128>{});
     return hipGetLastError();
 }
 
