@@ -8,7 +8,7 @@
 //     its (TH+2) x 34 input halo (zero outside the map) is staged in LDS once
 //     (144-byte pixel rows: conflict-free 32-pixel fragment reads);
 //   * wave w computes parity class w (GEMM rows 32w .. 32w+31) for every
-//     pixel of the block; its A fragments are read from L2 one tap ahead of
+//     pixel of the block; its A fragments are read from L2 two taps ahead of
 //     the MFMAs (four per tap), so the wave holds no full copy of A.  With A
 //     in fragment order (FRAG) each of those reads is one contiguous 1 KB
 //     (8 cache lines); tap-major A scatters it over 32 rows of A, 32 bytes
@@ -79,8 +79,9 @@ __global__ __launch_bounds__(256) void upconv64_kernel(ConvParams p, int tiles_x
     auto afrag = [&](int tap, int s) -> u32x4 {
         return *(const u32x4 *) (arow + (FRAG ? (tap * KS + s) * (4 * 64 * 8) : tap * IC + s * 16));
     };
-    u32x4 af[2][KS];
+    u32x4 af[3][KS];   // tap t's fragments in set t % 3, requested two taps ahead
     static_for<KS>([&](auto s) { af[0][s] = afrag(0, s); });
+    static_for<KS>([&](auto s) { af[1][s] = afrag(1, s); });
     static_for<PF>([&](auto i) {
         const int ch = tid + i * NT;
         if (ch < HCH) {
@@ -98,9 +99,9 @@ __global__ __launch_bounds__(256) void upconv64_kernel(ConvParams p, int tiles_x
     });
     static_for<9>([&](auto tap) {
         constexpr int dy = tap / 3, dx = tap % 3;  // halo offsets of the tap
-        constexpr int cur = tap & 1;
-        if constexpr (tap + 1 < 9)
-            static_for<KS>([&](auto s) { af[cur ^ 1][s] = afrag(tap + 1, s); });
+        constexpr int cur = tap % 3;
+        if constexpr (tap + 2 < 9)
+            static_for<KS>([&](auto s) { af[(tap + 2) % 3][s] = afrag(tap + 2, s); });
         static_for<KS>([&](auto s) {
             static_for<TH>([&](auto b) {
                 const u32x4 bf =
