@@ -163,6 +163,20 @@ int tpmd_decode_batch(tpmd_ctx *ctx, const float *styles, int n, float *imgs, in
  * buffer into it on the decoder's stream (a decode with taps set runs on
  * one lane), failing if `bytes` is too small.  tpmd_tap_frame_bytes gives
  * the bytes per frame, or -1 where the chain holds no such buffer. */
+/* The reference's tap plan for one frame (motion_dec::decode with a
+ * tap_sink after build(be, true), src/motion_dec.cpp:794-888 and
+ * :1162-1188; dumped by tools/tp-parity.cpp:252-282): the style [512]
+ * (host) is decoded through the per-stage entry points' f32 kernels (styled
+ * convs with f32 output, the standalone stage tail storing trunk and warp),
+ * and every tap is handed to cb as host f32 in the reference's names and
+ * torch layouts, in decode order: conv1_4 [1,C0,4,4]; then per stage
+ * r = 8 << j: r<r>.conv1, r<r>.conv2 [1,OC,r,r]; r<r>.flowmap [1,3,r,r];
+ * r<r>.grid [1,r,r,2]; r<r>.warp, r<r>.out [1,OC,r,r]; r<r>.rgb [1,3,r,r].
+ * data is valid during the call; a nonzero return stops with -1.  img
+ * (host [3][R][R], or NULL) receives the frame.  Synchronous. */
+typedef int (*tpmd_tap_cb)(const char *name, const float *data, int ndim, const int64_t *shape, void *ud);
+int tpmd_decode_taps(tpmd_ctx *ctx, const float *style, float *img, tpmd_tap_cb cb, void *ud);
+
 #define TPMD_TAP_TRUNK 0
 #define TPMD_TAP_C1 1
 #define TPMD_TAP_OUT 2

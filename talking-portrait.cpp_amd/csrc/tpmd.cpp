@@ -245,8 +245,8 @@ struct tpmd_ctx {
     bool any_tap = false;
 
     // scratch for the per-stage entry points (grow-only)
-    void *scr[4] = {};
-    size_t scr_sz[4] = {};
+    void *scr[13] = {};
+    size_t scr_sz[13] = {};
     // this device's static scratch (tpmd_modconv_static), or null + reason
     void *static_scratch = nullptr;
     std::string static_scratch_err;
@@ -1472,6 +1472,165 @@ static int tpmd_modconv_static_body(tpmd_ctx *c, int conv, const float *x, int n
     return modconv_run(c, cv, x, n, H, W, s, y, pick_stream(c, stream), xs, den, ws);
 }
 
+// tpmd_decode_taps: one frame through the unfused f32 chain (the per-stage
+// entry points' kernels: styled convs with f32 output, the standalone stage
+// tail storing trunk, warp, flow and rgb), every tap copied to the host in the
+// reference's tap layout
+static int tpmd_decode_taps_body(tpmd_ctx *c, const float *style, float *img, tpmd_tap_cb cb, void *ud) {
+    if (!check_ctx(c)) return -1;
+    if (!c->built || !c->feats_set) {
+        c->err = !c->built ? "decoder not built" : "feats not set";
+        return -1;
+    }
+    if (!style || !cb) {
+        c->err = "tpmd_decode_taps: null style or callback";
+        return -1;
+    }
+    if (!drain_lanes(c)) return -1;
+    for (auto &o : c->lane_out) o = tpmd_ctx::OutRange{};
+    hipStream_t st = c->stream;
+    tpmd_ctx::Lane &L = c->lane[0];
+    const int ns = c->ns, C0 = c->ic[0];
+    size_t mx = (size_t) 16 * C0;
+    for (int j = 0; j < ns; j++) mx = std::max(mx, (size_t) (8 << j) * (8 << j) * c->oc[j]);
+    const size_t R = (size_t) c->out_res(), skip = 3 * R * R;
+    // grid: the flow head's [3][r*r] output, then the identity grid [2][r*r]
+    float *buf[3], *warp = (float *) c->scratch(7, mx * 4), *grid = (float *) c->scratch(8, 5 * R * R * 4);
+    if (!warp || !grid) return -1;
+    for (int i = 0; i < 3; i++)
+        if (!(buf[i] = (float *) c->scratch(4 + i, mx * 4))) return -1;
+    // flow and rgb maps of every stage up to the last, 3 x R x R each (the
+    // lane's skip buffers hold only the stages before the last)
+    float *flow[2], *rgb[2];
+    for (int i = 0; i < 2; i++) {
+        flow[i] = (float *) c->scratch(9 + i, skip * 4);
+        rgb[i] = (float *) c->scratch(11 + i, skip * 4);
+        if (!flow[i] || !rgb[i]) return -1;
+    }
+    if (!c->hip_ok(hipMemcpyAsync(L.lat, style, 512 * 4, hipMemcpyHostToDevice, st), "style upload") ||
+        !c->hip_ok(launch_style_gemv(c->wmod, c->bmod, L.lat, L.s_all, c->seg, 1, st), "style") ||
+        !c->hip_ok(launch_demod(c->saug_all, L.s_all, L.den_all, c->dem, 1, st), "demod"))
+        return -1;
+    // the convs' scratch at its largest up front: no slot is reallocated while
+    // an earlier launch of this call may still read it
+    {
+        ModconvScratch big;
+        for (int L_ = 0; L_ < c->nconv; L_++) {
+            const ConvW &cv = c->conv[L_];
+            const int j = (L_ - 1) / 2;
+            const int H = L_ == 0 ? 4 : (cv.up ? 4 << j : 8 << j);
+            const ModconvScratch m = modconv_scratch(c, cv, 1, H, H);
+            big.xs = std::max(big.xs, m.xs);
+            big.den = std::max(big.den, m.den);
+            big.ws = std::max(big.ws, m.ws);
+        }
+        if (!c->scratch(1, big.xs) || !c->scratch(2, big.den) || (big.ws && !c->scratch(3, big.ws))) return -1;
+    }
+    std::vector<float> h((size_t) mx), t((size_t) mx);
+    // device CL [r*r][C] (or SP when sp) -> host, SP [1][C][r][r] -> callback
+    auto emit = [&](const char *name, const float *d, int C, int r, bool sp, std::vector<int64_t> shape) {
+        const size_t n = (size_t) r * r * C;
+        if (!c->hip_ok(hipMemcpyAsync(h.data(), d, n * 4, hipMemcpyDeviceToHost, st), "tap download") ||
+            !c->hip_ok(hipStreamSynchronize(st), "tap sync"))
+            return false;
+        const float *src = h.data();
+        if (!sp) {
+            for (size_t p = 0; p < (size_t) r * r; p++)
+                for (int ch = 0; ch < C; ch++) t[(size_t) ch * r * r + p] = h[p * C + ch];
+            src = t.data();
+        }
+        if (cb(name, src, (int) shape.size(), shape.data(), ud) != 0) {
+            if (c->err.empty()) c->err = std::string("tap callback stopped at ") + name;
+            return false;
+        }
+        return true;
+    };
+    auto conv = [&](int L_, const float *x, int H, float *y) {
+        const ConvW &cv = c->conv[L_];
+        const ModconvScratch m = modconv_scratch(c, cv, 1, H, H);
+        void *xs = c->scratch(1, m.xs);
+        float *den = (float *) c->scratch(2, m.den);
+        float *ws = m.ws ? (float *) c->scratch(3, m.ws) : nullptr;
+        if (!xs || !den || (m.ws && !ws)) return false;
+        return modconv_run(c, cv, x, 1, H, H, L.s_all + cv.s_off, y, st, xs, den, ws) == 0;
+    };
+    if (!conv(0, c->input_cl, 4, buf[0]) || !emit("conv1_4", buf[0], C0, 4, false, {1, C0, 4, 4})) return -1;
+    std::vector<float> xs;
+    char nm[32];
+    for (int j = 0; j < ns; j++) {
+        const int r = 8 << j, C = c->oc[j];
+        const int64_t r64 = r, C64 = C;
+        float *c1 = buf[1], *out = buf[2], *trunk = buf[0];
+        if (!conv(1 + 2 * j, buf[0], r / 2, c1)) return -1;
+        snprintf(nm, sizeof nm, "r%d.conv1", r);
+        if (!emit(nm, c1, C, r, false, {1, C64, r64, r64})) return -1;
+        if (!conv(2 + 2 * j, c1, r, out)) return -1;
+        snprintf(nm, sizeof nm, "r%d.conv2", r);
+        if (!emit(nm, out, C, r, false, {1, C64, r64, r64})) return -1;
+        const StageW &sw = c->st[j];
+        TailArgs a{};
+        a.out = out;
+        a.feat = sw.feat;
+        a.wflow = sw.wflow;
+        a.sflow = L.s_all + sw.s_off;
+        a.fbias = sw.fbias;
+        a.fup = sw.fup;
+        a.flow_prev = j > 0 ? flow[(j - 1) & 1] : nullptr;
+        a.flow_cur = flow[j & 1];
+        a.lin = sw.lin;
+        a.wrgb = sw.wrgb;
+        a.rlb = sw.rlb;
+        a.rbias = sw.rbias;
+        a.rup = sw.rup;
+        a.rgb_prev = j > 0 ? rgb[(j - 1) & 1] : nullptr;
+        a.rgb_cur = rgb[j & 1];
+        a.trunk = trunk;      // overwrites the stage input, read by the up-conv only
+        a.warp_tap = warp;
+        a.nframes = 1;
+        a.r = r;
+        a.C = C;
+        if (!c->hip_ok(launch_stage_tail(a, c->f16, false, false, st), "tail")) return -1;
+        snprintf(nm, sizeof nm, "r%d.flowmap", r);
+        if (!emit(nm, flow[j & 1], 3, r, true, {1, 3, r64, r64})) return -1;
+        // grid: the flow head on the identity grid (planar gx, gy), interleaved
+        xs.resize((size_t) 2 * r * r);
+        for (int y = 0; y < r; y++)
+            for (int x = 0; x < r; x++) {
+                xs[(size_t) y * r + x] = (float) (-1.0 + 2.0 * x / (r - 1));
+                xs[(size_t) r * r + (size_t) y * r + x] = (float) (-1.0 + 2.0 * y / (r - 1));
+            }
+        float *xs_d = grid + skip;
+        if (!c->hip_ok(hipMemcpyAsync(xs_d, xs.data(), xs.size() * 4, hipMemcpyHostToDevice, st), "grid upload") ||
+            !c->hip_ok(launch_flow_grid(flow[j & 1], xs_d, grid, (int64_t) r * r, st), "flow head"))
+            return -1;
+        // [3][r*r] planar -> [r*r][2] interleaved is the CL view of the first two planes
+        if (!c->hip_ok(hipMemcpyAsync(h.data(), grid, (size_t) 2 * r * r * 4, hipMemcpyDeviceToHost, st), "tap download") ||
+            !c->hip_ok(hipStreamSynchronize(st), "tap sync"))
+            return -1;
+        for (size_t p = 0; p < (size_t) r * r; p++) {
+            t[2 * p] = h[p];
+            t[2 * p + 1] = h[(size_t) r * r + p];
+        }
+        snprintf(nm, sizeof nm, "r%d.grid", r);
+        const int64_t gshape[4] = {1, r64, r64, 2};
+        if (cb(nm, t.data(), 4, gshape, ud) != 0) {
+            if (c->err.empty()) c->err = std::string("tap callback stopped at ") + nm;
+            return -1;
+        }
+        snprintf(nm, sizeof nm, "r%d.warp", r);
+        if (!emit(nm, warp, C, r, false, {1, C64, r64, r64})) return -1;
+        snprintf(nm, sizeof nm, "r%d.out", r);
+        if (!emit(nm, trunk, C, r, false, {1, C64, r64, r64})) return -1;
+        snprintf(nm, sizeof nm, "r%d.rgb", r);
+        if (!emit(nm, rgb[j & 1], 3, r, true, {1, 3, r64, r64})) return -1;
+    }
+    if (img) {
+        if (!c->hip_ok(hipMemcpyAsync(img, rgb[(ns - 1) & 1], skip * 4, hipMemcpyDeviceToHost, st), "image download"))
+            return -1;
+    }
+    return c->hip_ok(hipStreamSynchronize(st), "decode") ? 0 : -1;
+}
+
 static int tpmd_stage_tail_body(tpmd_ctx *c, int j, const float *out, int n, const float *s_flow, const float *flow_prev,
                     const float *rgb_prev, float *flow, float *trunk, float *rgb, float *warp,
                     void *stream) {
@@ -1674,6 +1833,10 @@ int tpmd_set_tap(tpmd_ctx *c, int kind, int stage, void *dst, int64_t bytes) {
 int tpmd_modconv(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,
                  void *stream) {
     return guarded(c, [&] { return tpmd_modconv_body(c, conv, x, n, H, W, s, y, stream); });
+}
+
+int tpmd_decode_taps(tpmd_ctx *c, const float *style, float *img, tpmd_tap_cb cb, void *ud) {
+    return guarded(c, [&] { return tpmd_decode_taps_body(c, style, img, cb, ud); });
 }
 
 int tpmd_modconv_static(tpmd_ctx *c, int conv, const float *x, int n, int H, int W, const float *s, float *y,

@@ -85,10 +85,6 @@ bool motion_dec::build(hip_backend &be, bool with_taps, std::string &err) {
         err = "motion_dec: build before prepare";
         return false;
     }
-    if (with_taps) {
-        err = "motion_dec: the tap plan (exact graph) is not available on the HIP decoder";
-        return false;
-    }
     int b = 8;
     if (const char *e = std::getenv("TP_MDEC_BATCH")) b = std::atoi(e);
     if (b < 1) b = 1;
@@ -96,7 +92,9 @@ bool motion_dec::build(hip_backend &be, bool with_taps, std::string &err) {
     if (tpmd_build(ctx, b) != 0) return fail(err, "build");
     batch = tpmd_batch(ctx);
     img_chunks = 1;
-    taps_in_graph = false;
+    // the tap plan (decode with a tap sink) runs beside the batched plan on
+    // the same buffers, so asking for it changes nothing else
+    taps_in_graph = with_taps;
     built = true;
     return true;
 }

@@ -16,13 +16,18 @@
 // library needs from them:
 //   backend_t   -> hip_backend   (device ordinal + ftype, src/backend.cpp:9-57)
 //   weights_t   -> weight_source (name -> raw f32 values, src/gguf_load.cpp)
-//   tap_sink    -> any type; taps come from the reference's exact graph
-//                  (src/motion_dec.cpp:794-888), which this library does not
-//                  run, so a decode that asks for taps fails with an error.
+//   tap_sink    -> any type with the reference's tap_sink members `wr` (a
+//                  tap_writer with add_f32(name, data, torch_shape) and `err`,
+//                  src/dump.h:13-24) and `prefix`, and its bool test: a
+//                  decode that asks for taps runs the library's tap plan
+//                  (tpmd_decode_taps) and writes the reference's tap names
+//                  (src/motion_dec.cpp:805-883) through it.
 // Error contract as the reference: false + err, no exceptions.
 #pragma once
 
 #include <string>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "tpmd.h"
@@ -54,7 +59,7 @@ struct motion_dec {
 
     tpmd_ctx *ctx = nullptr;
     bool built = false;
-    bool taps_in_graph = false;  // always false: no tap plan on the GPU
+    bool taps_in_graph = false;  // build(be, true) was asked for (decode then serves taps)
     int batch = 1;               // frames per decode_batch call
     int img_chunks = 0;          // 1 once the batched plan is built
     int res = 512;
@@ -74,11 +79,13 @@ struct motion_dec {
     bool decode(hip_backend &be, const float *style, float *img_out, std::string &err);
     template <class Tap>
     bool decode(hip_backend &be, const float *style, float *img_out, Tap &tap, std::string &err) {
-        if (tap) {
-            err = "motion_dec: taps need the exact graph, which the HIP decoder does not run";
+        if (!tap) return decode(be, style, img_out, err);
+        if constexpr (!has_tap_writer<Tap>::value) {
+            err = "motion_dec: taps need a sink with a tap writer (wr->add_f32) and a prefix";
             return false;
+        } else {
+            return decode_taps(style, img_out, tap, err);
         }
-        return decode(be, style, img_out, err);
     }
     bool decode_batch(hip_backend &be, const float *styles, float *imgs_out, std::string &err);
 
@@ -86,6 +93,37 @@ struct motion_dec {
     ~motion_dec() { release(); }
 
   private:
+    // Tap has the reference tap_sink's `wr` (with add_f32 and err) and `prefix`
+    template <class T, class = void>
+    struct has_tap_writer : std::false_type {};
+    template <class T>
+    struct has_tap_writer<T, std::void_t<decltype(std::declval<T &>().wr->add_f32(
+                                 std::declval<T &>().prefix + "", (const float *) nullptr,
+                                 std::vector<int64_t>()))>> : std::true_type {};
+    template <class Tap>
+    bool decode_taps(const float *style, float *img_out, Tap &tap, std::string &err) {
+        if (!ctx || !built) {
+            err = "decoder not built";
+            return false;
+        }
+        struct sink_t {
+            Tap *tap;
+            std::string err;
+        } sink{&tap, {}};
+        auto put = [](const char *name, const float *data, int ndim, const int64_t *shape, void *ud) -> int {
+            sink_t *s = (sink_t *) ud;
+            const std::vector<int64_t> sh(shape, shape + ndim);
+            if (s->tap->wr->add_f32(s->tap->prefix + name, data, sh)) return 0;
+            s->err = s->tap->wr->err;
+            return 1;
+        };
+        if (tpmd_decode_taps(ctx, style, img_out, put, &sink) != 0) {
+            err = !sink.err.empty() ? sink.err : tpmd_last_error(ctx);
+            return false;
+        }
+        return true;
+    }
+
     std::vector<size_t> feat_sizes;  // elements of feats[j] for this channel plan
     bool fail(std::string &err, const char *what);
 };

@@ -22,6 +22,7 @@
 // output then ends with appearance [512], lambda [20] and motion [512].
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -77,6 +78,35 @@ struct menc_like {  // the member of menc_result that set_feats reads
 
 struct no_taps {
     explicit operator bool() const { return false; }
+};
+
+// the reference's tap_writer / tap_sink pair (src/dump.h:13-24,
+// src/tp_internal.h:131-142) reduced to what motion_dec::decode uses: one raw
+// little-endian .f32 file per tap and a line "name d0 d1 ..." per tap in
+// meta.txt
+struct dir_writer {
+    std::string dir, err;
+    FILE *meta = nullptr;
+    bool add_f32(const std::string &name, const float *data, const std::vector<int64_t> &shape) {
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        FILE *f = fopen((dir + "/" + name + ".f32").c_str(), "wb");
+        if (!f || fwrite(data, 4, (size_t) n, f) != (size_t) n) {
+            err = "cannot write tap " + name;
+            if (f) fclose(f);
+            return false;
+        }
+        fclose(f);
+        fprintf(meta, "%s", name.c_str());
+        for (int64_t d : shape) fprintf(meta, " %lld", (long long) d);
+        fprintf(meta, "\n");
+        return true;
+    }
+};
+struct dir_sink {
+    dir_writer *wr = nullptr;
+    std::string prefix;
+    explicit operator bool() const { return wr != nullptr; }
 };
 
 }  // namespace
@@ -193,6 +223,25 @@ int main(int argc, char **argv) {
     if (!dec.decode(be, styles.data(), out.data() + (size_t) nf * fsz, tap, err)) {
         fprintf(stderr, "shim_check: %s\n", err.c_str());
         return 1;
+    }
+    // TPMD_SHIM_TAPS=<dir>: the tap plan of the first style, as tools/tp-parity
+    // asks for it (build with taps, then decode with a tap sink), its taps in
+    // <dir> and its frame appended to the output
+    if (const char *tdir = std::getenv("TPMD_SHIM_TAPS")) {
+        dir_writer wr;
+        wr.dir = tdir;
+        wr.meta = fopen((wr.dir + "/meta.txt").c_str(), "w");
+        dir_sink ts;
+        ts.wr = &wr;
+        ts.prefix = "mdec.f0.";
+        std::vector<float> timg(fsz);
+        if (!wr.meta || !dec.build(be, true, err) || !dec.set_feats(m, err) ||
+            !dec.decode(be, styles.data(), timg.data(), ts, err)) {
+            fprintf(stderr, "shim_check taps: %s\n", wr.meta ? err.c_str() : "cannot open meta.txt");
+            return 1;
+        }
+        fclose(wr.meta);
+        out.insert(out.end(), timg.begin(), timg.end());
     }
     if (with_enc) {
         out.insert(out.end(), mr.appearance.begin(), mr.appearance.end());

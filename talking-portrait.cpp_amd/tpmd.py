@@ -33,6 +33,8 @@ TAP_TRUNK, TAP_C1, TAP_OUT, TAP_FLOW, TAP_RGB = range(5)
 FRAME_F32 = 0
 FRAME_RGB24 = 1
 FRAME_CB = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p)
+TAP_CB = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int,
+                          ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p)
 
 
 class TpmdError(RuntimeError):
@@ -73,6 +75,7 @@ def lib():
             "tpmd_profile_stages": (I, [P, I]),
             "tpmd_stage_times": (I, [P, P, I]),
             "tpmd_set_tap": (I, [P, I, I, P, I64]),
+            "tpmd_decode_taps": (I, [P, P, P, P, P]),
             "tpmd_tap_frame_bytes": (I64, [P, I, I]),
             "tpmd_modconv": (I, [P, I, P, I, I, I, P, P, P]),
             "tpmd_modconv_static": (I, [P, I, P, I, I, I, P, P, P]),
@@ -163,6 +166,7 @@ class MotionDecoder:
             raise TpmdError("tpmd_create failed (see stderr)")
         self.h = ctypes.c_void_p(h)
         self.batch = 0
+        self.res = 8 << (n_stages - 1)
 
     def close(self):
         if getattr(self, "h", None):
@@ -297,6 +301,23 @@ class MotionDecoder:
         out = np.empty((3, self.res, self.res), np.float32)
         self._check(lib().tpmd_decode(self.h, _hptr(s), _hptr(out)))
         return out
+
+    def decode_taps(self, style):
+        """the reference's tap plan for one latent (tpmd_decode_taps): the
+        frame (3, R, R) and {tap name: float32 array in its torch shape}"""
+        s = np.ascontiguousarray(style, dtype=np.float32).reshape(512)
+        img = np.empty((3, self.res, self.res), np.float32)
+        taps = {}
+
+        def put(name, data, ndim, shape, ud):
+            sh = tuple(shape[i] for i in range(ndim))
+            n = int(np.prod(sh))
+            buf = (ctypes.c_float * n).from_address(data)
+            taps[name.decode()] = np.frombuffer(buf, np.float32).reshape(sh).copy()
+            return 0
+        cb = TAP_CB(put)
+        self._check(lib().tpmd_decode_taps(self.h, _hptr(s), _hptr(img), ctypes.cast(cb, ctypes.c_void_p), None))
+        return img, taps
 
     def sync(self):
         self._check(lib().tpmd_sync(self.h))

@@ -93,3 +93,22 @@ def test_batch_independent_bits(torch_cuda, ftype):
         same = (big == small[:n]).flatten(1).all(1).cpu().numpy()
         assert same.all(), (ftype, n, np.nonzero(~same)[0].tolist())
         del big
+
+
+def test_throughput_clip_frames(torch_cuda):
+    """the throughput configuration: a 250-frame clip (f16, reference widths)
+    through the frame output path in launches of 16 frames rotating over the
+    decoder's lanes (the ragged last launch holds 10): every frame equals the
+    same latent decoded in a 2-frame call, bit for bit"""
+    raw, lat, feats = synth.workload("iid", 250, "f16")
+    dec = tpmd.MotionDecoder("f16", 7)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(16)
+    dec.set_feats(feats)
+    clip = dec.decode_frames(lat, tpmd.FRAME_F32)
+    assert clip.shape == (250, 3, 512, 512)
+    bad = [t + i for t in range(0, 250, 2)
+           for i, f in enumerate(dec.decode_batch(lat[t:t + 2])) if not np.array_equal(f, clip[t + i])]
+    dec.close()
+    assert not bad, bad[:10]

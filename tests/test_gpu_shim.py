@@ -110,3 +110,31 @@ def test_shim_encoder_to_decoder(torch_cuda, tmp_path):
     dec.set_feats(r["feats"])
     want = np.concatenate([dec.decode_batch(lat[t:t + 2]) for t in range(0, 3, 2)])
     assert np.array_equal(frames[:3], want)
+
+
+def test_shim_serves_the_tap_plan(torch_cuda, tmp_path):
+    """tools/tp-parity's flow through the shim: build(be, true), then decode
+    with a tap sink (a tap_writer with add_f32 and a prefix): every tap lands
+    in the writer under the sink's prefix, the same bits as the binding's
+    tpmd_decode_taps"""
+    raw, lat, feats = synth.workload("smooth", 2, "f16", IC, OC)
+    blob, out, tdir = tmp_path / "in.blob", tmp_path / "out.f32", tmp_path / "taps"
+    tdir.mkdir()
+    write_blob(blob, raw, feats, lat, IC, OC, True)
+    env = dict(os.environ, TP_MDEC_BATCH="2", TPMD_SHIM_TAPS=str(tdir))
+    p = subprocess.run([SHIM, str(blob), str(out)], env=env, capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    got = np.fromfile(out, np.float32).reshape(-1, 3, 512, 512)
+    dec = tpmd.MotionDecoder("f16", len(IC), IC, OC)
+    dec.set_weights(raw)
+    dec.prepare()
+    dec.build(2)
+    dec.set_feats(feats)
+    img, taps = dec.decode_taps(lat[0])
+    assert np.array_equal(got[-1], img)
+    meta = [l.split() for l in (tdir / "meta.txt").read_text().splitlines()]
+    assert [m[0] for m in meta] == ["mdec.f0." + n for n in taps]
+    for m in meta:
+        name, shape = m[0][len("mdec.f0."):], tuple(int(d) for d in m[1:])
+        assert shape == taps[name].shape, name
+        assert np.array_equal(np.fromfile(tdir / (m[0] + ".f32"), np.float32).reshape(shape), taps[name]), name
