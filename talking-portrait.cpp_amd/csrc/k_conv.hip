@@ -307,7 +307,7 @@ int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int
         return A_ORDER_FRAG;
     if (mode == MODE_DENSE && H == W && f16 && OC == 256 && IC % 32 == 0 && modconv_fusable(OC, H, f16))
         return A_ORDER_RING_TAP;
-    if (modconv_hring_ok(f16, out_f16, mode, IC, OC, H, W)) return modconv_hring_frag_a ? A_ORDER_FRAG : A_ORDER_RING;
+    if (modconv_hfrag_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_FRAG;
     return A_ORDER_TAP;
 }
 
@@ -441,9 +441,9 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
         if (c.A_perm) p.A = c.A_perm;
         return launch_modconv_up64(p, c.A_perm != nullptr, st);
     }
-    if (!fused && c.A_perm && modconv_hring_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
+    if (!fused && c.A_perm && modconv_hfrag_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
         p.A = c.A_perm;
-        return launch_modconv_hring(p, c.mode, st);
+        return launch_modconv_hfrag(p, c.mode, st);
     }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);

@@ -447,214 +447,21 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
 }
 
 // ---------------------------------------------------------------------------
-// The same ring with the B operand read from an input halo instead of an
-// im2col tile (f16 output, every tile inside one frame): a tile is 256 GEMM
-// rows x an 8 x 32 block of pixels, and the k order is channel-chunk major,
-// k tile t = c*9 + tap (32 channels c*32 .. +31 of tap `tap`; A is stored in
-// that k order, laid out as the A DMA's LDS image, A_ORDER_RING).  Per chunk the 10 x 34 halo of those 32
-// channels is fetched once by the DMA path into one of two halo buffers
-// (80-byte pixels: 4 chunks of 8 channels + a pad chunk, so 32 consecutive
-// pixels read at any offset hit distinct banks), and its 9 taps read it
-// shifted by (dy, dx): the B bytes moved per chunk drop from 9 x 16 KB of
-// im2col rows to one 27 KB halo.  A still streams through the S-stage ring.
+// Halo up-conv / dense conv (f16 operands and output, every tile inside one
+// frame): a tile is 256 GEMM rows x an 8 x 32 block of pixels of one frame,
+// and the k order is channel-chunk major, k tile t = c*9 + tap (32 channels
+// c*32 .. +31 of tap `tap`).  Per chunk the 10 x 34 halo of those 32 channels
+// is fetched once into one of two LDS halo buffers (80-byte pixels: 4 chunks
+// of 8 channels + a pad chunk, so 32 consecutive pixels read at any offset
+// hit distinct banks), and its 9 taps read it shifted by (dy, dx): the B
+// bytes moved per chunk drop from 9 x 16 KB of im2col rows to one 27 KB halo.
 constexpr int HR_TH = 8, HR_TW = 32, HR_HWD = HR_TW + 2, HR_HPX = (HR_TH + 2) * HR_HWD;
 constexpr int HR_PXB = 80;              // halo pixel: 64 bytes of channels + 16-byte pad
-constexpr int HR_HBUF = 32 * 1024;      // one halo buffer: 32 DMA instructions of 1 KB
+constexpr int HR_HBUF = 32 * 1024;      // one halo buffer: 32 units of 1 KB
 static_assert(HR_HPX * HR_PXB <= HR_HBUF, "halo buffer");
 
-template <int S>
-struct hring_cfg {
-    static constexpr int BM = 256, BN = HR_TH * HR_TW, RB = 64;
-    static constexpr int ASTAGE = BM * RB;              // one k tile of A
-    static constexpr int HOFF = S * ASTAGE;             // two halo buffers after the A ring
-    static constexpr int CONV = HOFF + 2 * HR_HBUF;
-    static constexpr int ORS = BM * 2 + 16, OUT = BN * ORS;
-    static constexpr int LDS = CONV > OUT ? CONV : OUT;
-};
-
-template <int MODE, int S, int NW>
-__global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p, int tiles_x, int tiles_frame) {
-    typedef half_t TA;
-    typedef hring_cfg<S> C;
-    // NW = 8: 2 x 4 waves of 128 x 64; NW = 4: 2 x 2 waves of 128 x 128
-    // (accumulators in AGPRs, one wave per SIMD, 2/3 of the LDS fragment reads)
-    constexpr int BM = C::BM, BN = C::BN, WN = NW / 2, NT = NW * 64;
-    constexpr int RB = C::RB, BK = RB / 2;
-    constexpr int LPA = BM / 16 / NW;                  // A DMA instructions per wave per k tile
-    constexpr int LPH = HR_HBUF / 1024 / NW;           // halo DMA instructions per wave per chunk
-    constexpr int WTM = 128, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
-    static_assert(S >= 3 && S <= 8, "ring stages");
-    __shared__ __attribute__((aligned(16))) char smem[C::LDS];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wid = tid >> 6;
-    const int wm = wid / WN, wn = wid % WN;
-    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
-    const int mt = tile % p.MT, nt = tile / p.MT;
-    const int fr = nt / tiles_frame;
-    const int trem = nt - fr * tiles_frame;
-    const int ty = trem / tiles_x;
-    const int y0 = ty * HR_TH, x0 = (trem - ty * tiles_x) * HR_TW;
-    const int m0 = mt * BM;
-    const int IC = p.IC, H = p.H, W = p.W;
-    const int NC = IC / BK, T = 9 * NC;
-
-    // A DMA: instruction j of a wave moves the 16-row block g = m0/16 +
-    // wid*LPA + j; A is stored in that DMA's LDS image order (A_ORDER_RING:
-    // lane i carries chunk (i % 4) ^ swz(row) of row i / 4), so block (g, t)
-    // is 1 KB of contiguous memory at (g*T + t) KB
-    const TA *asrc[LPA];
-#pragma unroll
-    for (int j = 0; j < LPA; j++)
-        asrc[j] = (const TA *) p.A + ((int64_t) (m0 / 16 + wid * LPA + j) * T) * 512 + lane * 8;
-    // halo DMA: instruction h of a wave fills the 16-byte unit u = (wid*LPH + h)*64 + lane
-    // of a halo buffer: halo pixel u / 5, channel chunk u % 5 (4: the pad);
-    // units past the halo, pads and pixels outside the map read zeros
-    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
-    const TA *hsrc[LPH];
-    bool hok[LPH];
-#pragma unroll
-    for (int h = 0; h < LPH; h++) {
-        const int u = (wid * LPH + h) * 64 + lane;
-        const int hp = u / 5, q = u - hp * 5;
-        const int hy = hp / HR_HWD, hx = hp - hy * HR_HWD;
-        const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-        hok[h] = q < 4 && hp < HR_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
-        hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * IC + q * 8 : Xf;
-    }
-    const void *zero = (const void *) g_zero16;
-
-    auto issue_a = [&](int t) {
-        char *stage = smem + (t % S) * C::ASTAGE;
-        static_for<LPA>([&](auto j) {
-            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + t * 512),
-                                             TPMD_LDS(stage + (wid * LPA + j) * 16 * RB), 16, 0, 0);
-        });
-    };
-    auto issue_h = [&](int c) {
-        char *buf = smem + C::HOFF + (c & 1) * HR_HBUF;
-        static_for<LPH>([&](auto h) {
-            const void *g = hok[h] ? (const void *) (hsrc[h] + c * BK) : zero;
-            __builtin_amdgcn_global_load_lds(g, TPMD_LDS(buf + (wid * LPH + h) * 1024), 16, 0, 0);
-        });
-    };
-
-    floatx16 acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; a++)
-#pragma unroll
-        for (int b = 0; b < TN; b++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
-
-    const int lrow = lane & 31;
-    const int khalf = lane >> 5;
-    // this lane's halo pixel for tap (0, 0) of fragment b: block row TN*wn + b, column lrow
-    const int hbase = C::HOFF + ((TN * wn) * HR_HWD + lrow) * HR_PXB + khalf * 16;
-    auto read_frags = [&](int t, int ks, u32x4 (&af)[TM], u32x4 (&bf)[TN]) {
-        const char *st = smem + (t % S) * C::ASTAGE;
-        const int kc = ks * 2 + khalf;
-        static_for<TM>([&](auto a) {
-            const int row = wm * WTM + a * 32 + lrow;
-            af[a] = *(const u32x4 *) (st + row * RB + ((kc ^ swz(row)) << 4));
-        });
-        const int c = t / 9, tap = t - c * 9;
-        const int dy = tap / 3, dx = tap - dy * 3;
-        const char *hb = smem + hbase + (c & 1) * HR_HBUF + (dy * HR_HWD + dx) * HR_PXB + ks * 32;
-        static_for<TN>([&](auto b) { bf[b] = *(const u32x4 *) (hb + b * HR_HWD * HR_PXB); });
-    };
-    auto mfmas = [&](const u32x4 (&af)[TM], const u32x4 (&bf)[TN]) {
-        static_for<TM>([&](auto a) { static_for<TN>([&](auto b) { mfma_op<TA>::run(af[a], bf[b], acc[a][b]); }); });
-    };
-
-    // Software pipeline as in modconv3x3_async_kernel; the halo of chunk
-    // c+1 is requested at k tile 9c, right after that tile's A, once the
-    // barrier has retired every read of chunk c-1 (the buffer it reuses).
-    // A wait that needs A(t+1) leaves the tiles after it in flight, plus
-    // that halo when it was requested after A(t+1) (t - 9c in 1 .. S-2).
-    issue_h(0);
-#pragma unroll
-    for (int s = 0; s < S - 1; s++)
-        if (s < T) issue_a(s);
-    if (S - 2 < T) __builtin_amdgcn_s_waitcnt(waitcnt_vm((S - 2) * LPA));
-    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    u32x4 a0[TM], b0[TN], a1[TM], b1[TN];
-    read_frags(0, 0, a0, b0);
-    for (int t = 0; t < T; t++) {
-        read_frags(t, 1, a1, b1);
-        mfmas(a0, b0);
-        if (t + 1 < T) {
-            const int u = t % 9;
-            const bool halo_after = u >= 1 && u <= S - 2 && t / 9 + 1 < NC;
-            if (t + S - 2 < T) {
-                if (halo_after) __builtin_amdgcn_s_waitcnt(waitcnt_vm((S - 3) * LPA + LPH));
-                else __builtin_amdgcn_s_waitcnt(waitcnt_vm((S - 3) * LPA));
-            } else {
-                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-            }
-            __builtin_amdgcn_s_barrier();   // every wave's part landed, tile t-1 consumed
-            asm volatile("" ::: "memory");
-            if (t + S - 1 < T) issue_a(t + S - 1);
-            if (u == 0 && t / 9 + 1 < NC) issue_h(t / 9 + 1);
-            read_frags(t + 1, 0, a0, b0);
-        }
-        mfmas(a1, b1);
-    }
-
-    // f16 store epilogue through LDS (as modconv3x3_async_kernel): pixel nl
-    // of the tile is block row nl / 32, column nl % 32
-    __syncthreads();
-    static_for<TN>([&](auto b) {
-        const int nl = wn * WTN + b * 32 + lrow;
-        static_for<TM>([&](auto a) {
-            static_for<4>([&](auto i) {
-                const int ml = wm * WTM + a * 32 + i * 8 + (lane >> 5) * 4;
-                const int m = m0 + ml;
-                const int o = MODE == MODE_DENSE ? m : m % p.OC;
-                const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + o);
-                const floatx4 bb = *(const floatx4 *) (p.bias + o);
-                floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
-                if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
-                half4 hv;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float v = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
-                    if (p.out_scale) v *= sc[j];
-                    hv[j] = (half_t) v;
-                }
-                *(half4 *) (smem + nl * C::ORS + ml * 2) = hv;
-            });
-        });
-    });
-    __syncthreads();
-    constexpr int CPR = BM / 8, NCH = BN * CPR, STEP = NT / CPR;
-    static_assert(NCH % NT == 0 && NT % CPR == 0 && HR_TW % STEP == 0, "store pass");
-    const int mc = tid % CPR;
-    const int m = m0 + mc * 8;
-    int cls = 0, o = m;
-    if constexpr (MODE == MODE_SUBPIX) {
-        cls = m / p.OC;
-        o = m - cls * p.OC;
-    }
-    const int64_t HW = (int64_t) H * W;
-    half_t *Yp = (half_t *) p.Y;
-    static_for<NCH / NT>([&](auto j) {
-        const int nl = tid / CPR + j * STEP;
-        const int y = y0 + nl / HR_TW, x = x0 + nl % HR_TW;
-        int64_t opix;
-        if constexpr (MODE == MODE_DENSE) opix = fr * HW + (int64_t) y * W + x;
-        else opix = fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
-        const u32x4 v = *(const u32x4 *) (smem + nl * C::ORS + mc * 16);
-        *(u32x4 *) (Yp + opix * p.OC + o) = v;
-    });
-}
-
-// ---------------------------------------------------------------------------
-// The halo ring with A read by every wave straight from L2 in MFMA fragment
-// order (A_ORDER_FRAG: each fragment is one contiguous 1 KB) instead of
-// through an LDS ring.  Waves are 4 x 2 with 64 x 128 tiles, so a wave reads
+// A is read by every wave straight from L2 in MFMA fragment order
+// (A_ORDER_FRAG: each fragment is one contiguous 1 KB), not through LDS.  Waves are 4 x 2 with 64 x 128 tiles, so a wave reads
 // 2 A fragments and 4 B fragments per 16-wide k step.  The two waves that
 // share A rows read the same lines, and the second finds them in L1.  The LDS
 // holds only the two halo buffers, so the one barrier per 32-channel chunk
@@ -665,8 +472,6 @@ __global__ __launch_bounds__(NW * 64) void modconv3x3_hring_kernel(ConvParams p,
 //     current step's MFMAs run;
 //   * the halo of chunk c+1 is loaded into registers early in chunk c and
 //     written to the other LDS buffer late in it; one barrier ends the chunk.
-// The k order (chunk, tap, 16-wide step) is the hring kernel's, so the sums
-// are the same bits.
 template <int MODE, int NC>
 __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int tiles_x, int tiles_frame) {
     typedef half_t TA;
@@ -705,7 +510,9 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
         static_for<2>([&](auto s) { static_for<TM>([&](auto a) { dst[a][s] = afrag(tap, 2 * c + s, a); }); });
     };
 
-    // halo DMA, as modconv3x3_hring_kernel
+    // halo unit u = (wid*LPH + h)*64 + lane of a halo buffer: halo pixel u / 5,
+    // channel chunk u % 5 (4: the pad); units past the halo, pads and pixels
+    // outside the map read zeros
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     const TA *hsrc[LPH];
     bool hok[LPH];
@@ -784,7 +591,8 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
         if constexpr (c + 1 < NC) __syncthreads();   // halo c+1 written, chunk c's reads done
     });
 
-    // f16 store epilogue through LDS, as modconv3x3_hring_kernel
+    // f16 store epilogue: the tile is staged in LDS as [pixel][row] (528-byte
+    // rows) and written back as whole 16-byte chunks of contiguous output
     __syncthreads();
     static_for<TN>([&](auto b) {
         const int nl = (wn * TN + b) * 32 + lrow;
@@ -831,54 +639,42 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     });
 }
 
-// the 256-row halo ring: f16 operands and output, M a multiple of 256, input
-// maps of 8 x 32 blocks, and enough tiles at 16 frames to give every CU one
-bool modconv_hring_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
+// the 256-row halo kernel: f16 operands and output, M a multiple of 256, IC a
+// power of two from 32 to 512, input maps of 8 x 32 blocks, and enough tiles
+// at 16 frames to give every CU one
+bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
     const int M = mode == MODE_DENSE ? OC : 4 * OC;
-    if (!f16 || !out_f16 || IC % 32 != 0 || M % 256 != 0 || H % HR_TH != 0 || W % HR_TW != 0) return false;
-    if (modconv_hring_frag_a && IC != 32 && IC != 64 && IC != 128 && IC != 256 && IC != 512) return false;
+    if (!f16 || !out_f16 || M % 256 != 0 || H % HR_TH != 0 || W % HR_TW != 0) return false;
+    if (IC != 32 && IC != 64 && IC != 128 && IC != 256 && IC != 512) return false;
     return (int64_t) (M / 256) * 16 * (H / HR_TH) * (W / HR_TW) >= 256;
 }
 
-hipError_t launch_modconv_hring(ConvParams p, int mode, hipStream_t st) {
-    constexpr int S = 6;  // 16 KB A stages: six fill the LDS with the two halo buffers (measured: 4 -> 6 saves ~3%)
-    // 8 waves: 4 waves of 128 x 128 (one per SIMD) measured 6-15 % slower on
-    // the r64-r256 up-convs, each barrier left with no other wave to cover it
-    constexpr int NW = 8;
-    if (p.M % 256 != 0 || p.IC % 32 != 0 || p.H % HR_TH != 0 || p.W % HR_TW != 0) return hipErrorInvalidValue;
+hipError_t launch_modconv_hfrag(ConvParams p, int mode, hipStream_t st) {
+    if (p.M % 256 != 0 || p.H % HR_TH != 0 || p.W % HR_TW != 0) return hipErrorInvalidValue;
     const int64_t HW = (int64_t) p.H * p.W;
     if (p.N % HW != 0) return hipErrorInvalidValue;
     p.MT = p.M / 256;
     p.T = 9 * p.IC / 32;
     const int tiles_x = p.W / HR_TW, tiles_frame = tiles_x * (p.H / HR_TH);
     const int64_t tiles = (int64_t) p.MT * (p.N / HW) * tiles_frame;
-    if (modconv_hring_frag_a) {
-        auto go = [&](auto nc) {
-            constexpr int NC = decltype(nc)::value;
-            if (mode == MODE_DENSE)
-                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC>), dim3((unsigned) tiles), dim3(512), 0,
-                                   st, p, tiles_x, tiles_frame);
-            else
-                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC>), dim3((unsigned) tiles), dim3(512), 0,
-                                   st, p, tiles_x, tiles_frame);
-            return hipGetLastError();
-        };
-        switch (p.IC) {
-            case 32: return go(std::integral_constant<int, 1>{});
-            case 64: return go(std::integral_constant<int, 2>{});
-            case 128: return go(std::integral_constant<int, 4>{});
-            case 256: return go(std::integral_constant<int, 8>{});
-            case 512: return go(std::integral_constant<int, 16>{});
-            default: return hipErrorInvalidValue;
-        }
+    auto go = [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (mode == MODE_DENSE)
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC>), dim3((unsigned) tiles), dim3(512), 0, st, p,
+                               tiles_x, tiles_frame);
+        else
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC>), dim3((unsigned) tiles), dim3(512), 0, st,
+                               p, tiles_x, tiles_frame);
+        return hipGetLastError();
+    };
+    switch (p.IC) {
+        case 32: return go(std::integral_constant<int, 1>{});
+        case 64: return go(std::integral_constant<int, 2>{});
+        case 128: return go(std::integral_constant<int, 4>{});
+        case 256: return go(std::integral_constant<int, 8>{});
+        case 512: return go(std::integral_constant<int, 16>{});
+        default: return hipErrorInvalidValue;
     }
-    if (mode == MODE_DENSE)
-        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_DENSE, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0, st,
-                           p, tiles_x, tiles_frame);
-    else
-        hipLaunchKernelGGL((modconv3x3_hring_kernel<MODE_SUBPIX, S, NW>), dim3((unsigned) tiles), dim3(NW * 64), 0,
-                           st, p, tiles_x, tiles_frame);
-    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

@@ -485,19 +485,7 @@ std::vector<float> make_saug(const std::vector<float> &W, int OC, int IC) {
     return s;
 }
 
-// A [M][9*IC] (k = tap*IC + ic) -> [M][IC/32][9][32] (k = (ic/32*9 + tap)*32 + ic%32)
-std::vector<float> chunk_major(const std::vector<float> &A, int M, int IC) {
-    const size_t K = (size_t) 9 * IC;
-    std::vector<float> out(A.size());
-    for (int m = 0; m < M; m++)
-        for (int c = 0; c < IC / 32; c++)
-            for (int tap = 0; tap < 9; tap++)
-                for (int i = 0; i < 32; i++)
-                    out[m * K + ((size_t) c * 9 + tap) * 32 + i] = A[m * K + (size_t) tap * IC + c * 32 + i];
-    return out;
-}
-
-// A [M][K = 9*IC] in some k order -> the LDS rings' DMA order [M/16][T = K/32][64][8]:
+// A [M][K = 9*IC] (tap-major k) -> the LDS ring's DMA order [M/16][T = K/32][64][8]:
 // block (g, t), lane i = row 16g + i/4, chunk (i%4) ^ swz(row) of k tile t
 // (the row-swizzled LDS image the DMA writes)
 std::vector<float> dma_image(const std::vector<float> &ck, int M, int IC) {
@@ -514,8 +502,6 @@ std::vector<float> dma_image(const std::vector<float> &ck, int M, int IC) {
             }
     return out;
 }
-// the halo ring's copy: channel-chunk-major k; the fused r64 ring's: tap-major k
-std::vector<float> ring_order(const std::vector<float> &A, int M, int IC) { return dma_image(chunk_major(A, M, IC), M, IC); }
 
 // A [M][9*IC] (k = tap*IC + ic) -> MFMA fragment order [9][IC/16][M/32][64][8]:
 // fragment (tap, ks) of row block w, lane l = row 32w + l%32, k = tap*IC + ks*16 + (l/32)*8 + e
@@ -741,9 +727,7 @@ static int tpmd_prepare_body(tpmd_ctx *c) {
         const int order = modconv_a_order(c->f16, true, cv.up ? 1 : 0, cv.ic, cv.oc, hin, hin);
         if (order != A_ORDER_TAP) {
             const int M = cv.up ? 4 * cv.oc : cv.oc;
-            cv.A_perm = c->upload_act(order == A_ORDER_RING       ? ring_order(A, M, cv.ic)
-                                      : order == A_ORDER_RING_TAP ? dma_image(A, M, cv.ic)
-                                                                  : fragment_order(A, M, cv.ic));
+            cv.A_perm = c->upload_act(order == A_ORDER_RING_TAP ? dma_image(A, M, cv.ic) : fragment_order(A, M, cv.ic));
             if (!cv.A_perm) return -1;
         }
         cv.bias = c->upload(ab->data);

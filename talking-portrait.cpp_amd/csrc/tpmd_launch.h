@@ -97,19 +97,18 @@ int modconv_k_align(bool f16);
 // the order in which the kernel chosen for a conv shape reads A best
 // (ConvArgs::A_perm holds that copy; a function of the per-frame shape only):
 //   A_ORDER_TAP    [M][9][IC], A itself (no copy);
-//   A_ORDER_RING   [M/16][9*IC/32][64][8], the halo ring's LDS image of each
-//                  block of 16 rows x one k tile (channel-chunk-major k tiles
-//                  t = c*9 + tap of 32 channels; lane i = row 16g + i/4, k
-//                  chunk (i%4) ^ ((row>>2 ^ row>>3) & 3)), so each A DMA
-//                  instruction reads 1 KB of contiguous memory;
 //   A_ORDER_FRAG   [9][IC/16][M/32][64][8], MFMA fragment order: fragment
 //                  (tap, ks) of row block w at lane l holds row 32w + l%32,
-//                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the 64 -> 32 up-conv
-//                  and the fused 32- and 64-channel dense convs), so a wave
-//                  reads each fragment as one contiguous 1 KB.
-//   A_ORDER_RING_TAP  the same image over tap-major k tiles (the fused
-//                  256-channel dense conv's LDS ring, r64).
-enum { A_ORDER_TAP = 0, A_ORDER_RING = 1, A_ORDER_FRAG = 2, A_ORDER_RING_TAP = 3 };
+//                  k = tap*IC + ks*16 + (l/32)*8 .. +8 (the halo up-convs,
+//                  the 64 -> 32 up-conv and the fused 32- to 128-channel
+//                  dense convs), so a wave reads each fragment as one
+//                  contiguous 1 KB;
+//   A_ORDER_RING_TAP  [M/16][9*IC/32][64][8], the LDS image of each block of
+//                  16 rows x one tap-major k tile of 32 channels (lane i =
+//                  row 16g + i/4, k chunk (i%4) ^ ((row>>2 ^ row>>3) & 3)),
+//                  so each A DMA instruction of the fused 256-channel dense
+//                  conv's LDS ring (r64) reads 1 KB of contiguous memory.
+enum { A_ORDER_TAP = 0, A_ORDER_FRAG = 2, A_ORDER_RING_TAP = 3 };
 int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 // whether the dense conv of an r x r stage with OC channels fuses the tail
 bool modconv_fusable(int OC, int r, bool f16);
