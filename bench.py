@@ -337,6 +337,8 @@ def main():
                          "one stream (kernel traces comparable with the per-stage events)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run the 256 MiB calibration copy (for counter runs)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="enqueue each launch chain launch by launch instead of replaying it as a HIP graph")
     ap.add_argument("--decoder-only", action="store_true",
                     help="skip the frame-path, encoder, FMT and gather legs (for counter runs)")
     args = ap.parse_args()
@@ -366,6 +368,8 @@ def main():
     torch.cuda.synchronize()   # inputs resident before the decoder stream reads them
     if args.lanes == 1:
         dec.use_stream(torch.cuda.current_stream())   # a caller's stream: one lane
+    if args.no_graphs:
+        dec.use_graphs(False)
 
     def step(k):
         t0 = (k * B) % n_seq
@@ -421,6 +425,7 @@ def main():
         "stages": stages,
         "stage_sum_us": round(float(us.sum()), 1),
         "lanes": args.lanes,
+        "graphs": not args.no_graphs,
     }
     if args.decoder_only:
         if args.copy_probe:

@@ -220,6 +220,17 @@ int tpmd_sync(tpmd_ctx *ctx);
  * callers that share device buffers with other stream users need this
  * ordering. */
 int tpmd_set_stream(tpmd_ctx *ctx, void *stream);
+/* Whether decode_batch / decode_frames replay each lane's launch chain as a
+ * HIP graph (captured on the first call for a frame count and frame buffer,
+ * up to 4 per lane kept) instead of enqueuing its launches one by one;
+ * frames are the same bits either way.  On by default; TPMD_GRAPHS=0 in the
+ * environment at tpmd_create turns it off.  Waits for work in flight.  No
+ * entry point of the reference: there ggml-cuda's build option
+ * GGML_CUDA_GRAPHS decides whether a graph's launches are captured as a
+ * CUDA graph (off in its cuda preset, CMakePresets.json:24-33; its
+ * steady-state allocation check expects capture, bench/tp-allocproof.cpp:
+ * 103-107). */
+int tpmd_set_graphs(tpmd_ctx *ctx, int enable);
 
 /* Per-stage timing of the next decode_batch: when enabled, the call records
  * HIP events around each launch group and stores microseconds into

@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <new>
@@ -253,6 +254,27 @@ struct tpmd_ctx {
 
     bool profile = false;
 
+    // each lane's launch chain captured as HIP graphs, one per (frames,
+    // frame buffer) in use, replayed with one launch; kGraphs per lane, the
+    // least recently used replaced (TPMD_GRAPHS=0 in the environment, or
+    // tpmd_set_graphs, turns them off)
+    bool use_graphs = true;
+    static constexpr int kGraphs = 4;
+    struct Graph {
+        hipGraphExec_t exec = nullptr;
+        int n = 0;
+        const float *dst = nullptr;
+        uint64_t used = 0;
+    } graphs[kLanes][kGraphs];
+    uint64_t graph_clock = 0;
+    void drop_graphs() {
+        for (auto &lg : graphs)
+            for (auto &g : lg) {
+                if (g.exec) (void) hipGraphExecDestroy(g.exec);
+                g = Graph{};
+            }
+    }
+
     // frame streaming (tpmd_decode_frames): one device frame slot per lane,
     // pinned host staging, a copy stream and events; made by the first call
     struct {
@@ -335,6 +357,7 @@ struct tpmd_ctx {
         for (hipStream_t ls : lane_stream)
             if (ls) (void) hipStreamSynchronize(ls);
         if (own_stream) (void) hipStreamSynchronize(own_stream);
+        drop_graphs();
         for (auto e : ev) (void) hipEventDestroy(e);
         for (void *p : allocs) (void) hipFree(p);
         for (void *p : batch_allocs) (void) hipFree(p);
@@ -617,6 +640,7 @@ static tpmd_ctx *tpmd_create_body(int device, const char *ftype, int n_stages, c
     }
     c->stream = c->own_stream;
     c->static_scratch = static_scratch_of(device, c->static_scratch_err);
+    if (const char *g = std::getenv("TPMD_GRAPHS")) c->use_graphs = std::strcmp(g, "0") != 0;
     return c;
 }
 
@@ -673,7 +697,8 @@ const char *tpmd_weight_name(const tpmd_ctx *c, int i, int64_t *n, int *is_matri
 
 static int tpmd_prepare_body(tpmd_ctx *c) {
     if (!check_ctx(c)) return -1;
-    if (!drain_lanes(c)) return -1;
+    if (!drain_all(c)) return -1;
+    c->drop_graphs();
     for (void *p : c->allocs) (void) hipFree(p);
     c->allocs.clear();
     c->prepared = false;
@@ -779,7 +804,8 @@ static int tpmd_prepare_body(tpmd_ctx *c) {
 
 static int tpmd_build_body(tpmd_ctx *c, int max_batch) {
     if (!check_ctx(c)) return -1;
-    if (!drain_lanes(c)) return -1;
+    if (!drain_all(c)) return -1;
+    c->drop_graphs();
     if (!c->prepared) {
         c->err = "decoder not prepared";
         return -1;
@@ -1078,6 +1104,46 @@ static bool enqueue_decode(tpmd_ctx *c, int n, float *img_dst, hipEvent_t frames
     return true;
 }
 
+// enqueue_decode as one graph launch: the current lane's chain for (n,
+// img_dst) is captured on first use and replayed after that.  The graph
+// holds kernel launches only (no memsets, no copies).  Per-stage profiling,
+// taps, a stream that is itself being captured, or graphs turned off
+// enqueue the launches directly; `frames_after` then orders the whole graph
+// instead of its last stage.
+static bool run_chain(tpmd_ctx *c, int n, float *img_dst, hipEvent_t frames_after = nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!c->use_graphs || c->profile || c->any_tap || !c->stream ||
+        hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return enqueue_decode(c, n, img_dst, frames_after);
+    auto &lg = c->graphs[c->L - c->lane];
+    tpmd_ctx::Graph *g = nullptr, *lru = &lg[0];
+    for (auto &e : lg) {
+        if (e.exec && e.n == n && e.dst == img_dst) g = &e;
+        if (e.used < lru->used) lru = &e;
+    }
+    if (!g) {
+        g = lru;
+        if (g->exec) (void) hipGraphExecDestroy(g->exec);
+        *g = tpmd_ctx::Graph{};
+        if (!c->hip_ok(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph capture"))
+            return false;
+        const bool ok = enqueue_decode(c, n, img_dst);
+        hipGraph_t graph = nullptr;
+        const hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        hipGraphExec_t exec = nullptr;
+        const bool made = ok && c->hip_ok(e, "graph capture") &&
+                          c->hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+        if (graph) (void) hipGraphDestroy(graph);
+        if (!made) return false;
+        g->exec = exec;
+        g->n = n;
+        g->dst = img_dst;
+    }
+    g->used = ++c->graph_clock;
+    if (frames_after && !c->hip_ok(hipStreamWaitEvent(c->stream, frames_after, 0), "wait")) return false;
+    return c->hip_ok(hipGraphLaunch(g->exec, c->stream), "graph launch");
+}
+
 static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *imgs, int on_device,
                              int lane = -1);
 
@@ -1152,7 +1218,7 @@ static int decode_batch_lane(tpmd_ctx *c, const float *styles, int n, float *img
             after = c->ev_done[l];
         }
     }
-    if (!enqueue_decode(c, n, dst, after)) return -1;
+    if (!run_chain(c, n, dst, after)) return -1;
     if (lane >= 0) {
         if (!c->hip_ok(hipEventRecord(c->ev_done[lane], c->stream), "event")) return -1;
         c->lane_out[lane] = {lo, hi};
@@ -1270,9 +1336,9 @@ static int64_t tpmd_decode_frames_body(tpmd_ctx *c, const float *styles, int64_t
                                             hipMemcpyHostToDevice, c->stream),
                              "style upload");
         if (format == TPMD_FRAME_F32) {
-            ok = ok && enqueue_decode(c, nk, (float *) f.dev[s]);
+            ok = ok && run_chain(c, nk, (float *) f.dev[s]);
         } else {
-            ok = ok && enqueue_decode(c, nk, c->L->img) &&
+            ok = ok && run_chain(c, nk, c->L->img) &&
                  c->hip_ok(launch_rgb24(c->L->img, nk, (int) R, (uint8_t *) f.dev[s], c->stream), "rgb24");
         }
         ok = ok && c->hip_ok(hipEventRecord(f.computed[s], c->stream), "event") &&
@@ -1308,6 +1374,14 @@ int tpmd_set_stream(tpmd_ctx *c, void *stream) {
     if (c->stream != c->own_stream && !c->hip_ok(hipStreamSynchronize(c->stream), "stream sync")) return -1;
     for (auto &o : c->lane_out) o = tpmd_ctx::OutRange{};
     c->stream = (hipStream_t) stream;
+    return 0;
+}
+
+int tpmd_set_graphs(tpmd_ctx *c, int enable) {
+    if (!check_ctx(c)) return -1;
+    if (!drain_all(c)) return -1;
+    c->drop_graphs();
+    c->use_graphs = enable != 0;
     return 0;
 }
 

@@ -20,6 +20,14 @@
 // [3][512][512] CHW), tp::motion_enc runs on it and its menc_result replaces
 // the blob's feats (the generation flow, src/pipeline.cpp:113-115); the
 // output then ends with appearance [512], lambda [20] and motion [512].
+//
+// TPMD_SHIM_ALLOCS=<frames> in the environment: after the above, count the
+// heap allocations (malloc / calloc / realloc, operator new included) that
+// this thread makes in steady state, the way the reference's zero-allocation
+// check does (bench/tp-allocproof.cpp:121-150): two warm-up decode() calls,
+// then <frames> single-frame decode() calls, counted one by one; then two
+// warm-up and 20 counted decode_batch() calls.  Printed as "allocs ..." lines.
+#include <atomic>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -31,6 +39,36 @@
 #include "gguf.h"
 #include "motion_dec.h"
 #include "motion_enc.h"
+
+// ---- counting allocator: allocations of the main thread while counting
+// is on; every call goes on to glibc's own allocator
+extern "C" void *__libc_malloc(size_t);
+extern "C" void *__libc_calloc(size_t, size_t);
+extern "C" void *__libc_realloc(void *, size_t);
+extern "C" void __libc_free(void *);
+
+namespace {
+std::atomic<bool> g_counting{false};
+std::atomic<long> g_allocs{0};
+thread_local bool t_counted = false;
+inline void note_alloc() {
+    if (t_counted && g_counting.load(std::memory_order_relaxed)) g_allocs.fetch_add(1, std::memory_order_relaxed);
+}
+}  // namespace
+
+extern "C" void *malloc(size_t n) {
+    note_alloc();
+    return __libc_malloc(n);
+}
+extern "C" void *calloc(size_t n, size_t m) {
+    note_alloc();
+    return __libc_calloc(n, m);
+}
+extern "C" void *realloc(void *p, size_t n) {
+    note_alloc();
+    return __libc_realloc(p, n);
+}
+extern "C" void free(void *p) { __libc_free(p); }
 
 namespace {
 
@@ -223,6 +261,41 @@ int main(int argc, char **argv) {
     if (!dec.decode(be, styles.data(), out.data() + (size_t) nf * fsz, tap, err)) {
         fprintf(stderr, "shim_check: %s\n", err.c_str());
         return 1;
+    }
+    if (const char *na = std::getenv("TPMD_SHIM_ALLOCS")) {
+        const int frames = atoi(na) > 0 ? atoi(na) : 100;
+        std::vector<float> img(fsz);
+        t_counted = true;
+        auto counted = [&](auto &&call, long &total, long &worst) {
+            g_allocs = 0;
+            g_counting = true;
+            const bool ok = call();
+            g_counting = false;
+            const long a = g_allocs.load();
+            total += a;
+            worst = a > worst ? a : worst;
+            return ok;
+        };
+        long d_total = 0, d_worst = 0, b_total = 0, b_worst = 0, warm = 0, warm_worst = 0;
+        bool ok = true;
+        for (int f = 0; f < frames + 2 && ok; f++) {
+            const float *st = styles.data() + (size_t) (f % (int) nf) * 512;
+            auto call = [&] { return dec.decode(be, st, img.data(), tap, err); };
+            ok = f < 2 ? counted(call, warm, warm_worst) : counted(call, d_total, d_worst);
+        }
+        const int calls = 20;
+        for (int k = 0; k < calls + 2 && ok; k++) {
+            auto call = [&] { return dec.decode_batch(be, bst.data(), bimg.data(), err); };
+            ok = k < 2 ? counted(call, warm, warm_worst) : counted(call, b_total, b_worst);
+        }
+        t_counted = false;
+        if (!ok) {
+            fprintf(stderr, "shim_check allocs: %s\n", err.c_str());
+            return 1;
+        }
+        printf("allocs decode: %ld over %d frames, max %ld per frame\n", d_total, frames, d_worst);
+        printf("allocs decode_batch: %ld over %d calls of %d frames, max %ld per call\n", b_total, calls, BQ,
+               b_worst);
     }
     // TPMD_SHIM_TAPS=<dir>: the tap plan of the first style, as tools/tp-parity
     // asks for it (build with taps, then decode with a tap sink), its taps in

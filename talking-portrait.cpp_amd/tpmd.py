@@ -72,6 +72,7 @@ def lib():
             "tpmd_frames_to_rgb24": (I, [P, I, I, P, P]),
             "tpmd_sync": (I, [P]),
             "tpmd_set_stream": (I, [P, P]),
+            "tpmd_set_graphs": (I, [P, I]),
             "tpmd_profile_stages": (I, [P, I]),
             "tpmd_stage_times": (I, [P, P, I]),
             "tpmd_set_tap": (I, [P, I, I, P, I64]),
@@ -251,6 +252,8 @@ class MotionDecoder:
         for t, what in ((styles_dev, "styles"), (imgs_dev, "imgs")):
             if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32):
                 raise TpmdError(f"decode_batch_device: {what} must be a float32 CUDA tensor")
+            if not t.is_contiguous():
+                raise TpmdError(f"decode_batch_device: {what} must be contiguous")
         if styles_dev.dim() != 2 or styles_dev.shape[1] != 512:
             raise TpmdError("decode_batch_device: styles must be (n, 512)")
         n = styles_dev.shape[0]
@@ -326,6 +329,11 @@ class MotionDecoder:
         """enqueue the decoder's work on `stream` (torch stream or handle;
         None = torch's current stream)"""
         self._check(lib().tpmd_set_stream(self.h, _stream(stream)))
+
+    def use_graphs(self, enable=True):
+        """replay each lane's launch chain as a HIP graph (default) or
+        enqueue its launches one by one"""
+        self._check(lib().tpmd_set_graphs(self.h, 1 if enable else 0))
 
     def profile_stages(self, enable=True):
         return lib().tpmd_profile_stages(self.h, 1 if enable else 0)

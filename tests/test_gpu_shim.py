@@ -138,3 +138,34 @@ def test_shim_serves_the_tap_plan(torch_cuda, tmp_path):
         name, shape = m[0][len("mdec.f0."):], tuple(int(d) for d in m[1:])
         assert shape == taps[name].shape, name
         assert np.array_equal(np.fromfile(tdir / (m[0] + ".f32"), np.float32).reshape(shape), taps[name]), name
+
+
+def _steady_allocs(tmp_path, graphs):
+    """heap allocations per single-frame decode() and per decode_batch() call
+    of the shim in steady state, counted on the calling thread as the
+    reference's zero-allocation check counts them (bench/tp-allocproof.cpp:
+    121-150)"""
+    import re
+    raw, lat, feats = synth.workload("smooth", 8, "f16", IC, OC)
+    blob, out = tmp_path / f"a{int(graphs)}.blob", tmp_path / f"a{int(graphs)}.f32"
+    write_blob(blob, raw, feats, lat, IC, OC, True)
+    env = dict(os.environ, TPMD_SHIM_ALLOCS="50", TPMD_GRAPHS="1" if graphs else "0")
+    p = subprocess.run([SHIM, str(blob), str(out)], env=env, capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    d = re.search(r"allocs decode: (\d+) over (\d+) frames, max (\d+)", p.stdout)
+    b = re.search(r"allocs decode_batch: (\d+) over (\d+) calls of (\d+) frames, max (\d+)", p.stdout)
+    assert d and b, p.stdout
+    per_frame = int(d.group(1)) / int(d.group(2))
+    per_batch = int(b.group(1)) / int(b.group(2))
+    return per_frame, per_batch, int(b.group(3))
+
+
+def test_shim_steady_state_allocations(torch_cuda, tmp_path):
+    """the launch chain replayed as a HIP graph makes fewer host allocations
+    per decode than launch-by-launch enqueueing (the HIP runtime allocates a
+    host command object per enqueued operation; the library itself none)"""
+    g_frame, g_batch, B = _steady_allocs(tmp_path, True)
+    d_frame, d_batch, _ = _steady_allocs(tmp_path, False)
+    print(f"heap allocations, graphs: {g_frame:.1f} per decode(), {g_batch:.1f} per decode_batch({B}); "
+          f"direct launches: {d_frame:.1f} per decode(), {d_batch:.1f} per decode_batch({B})")
+    assert g_frame < d_frame and g_batch < d_batch
