@@ -383,7 +383,7 @@ hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool 
                        tiles_frame)
 #define TPMD_L(TT, FR)                               \
     do {                                             \
-        if (ta.featg) TPMD_L2(TT, FR, true);         \
+        if (ta.featg && !ta.trunk && !ta.warp_tap) TPMD_L2(TT, FR, true); \
         else TPMD_L2(TT, FR, false);                 \
     } while (0)
     if (trunk_f16) {

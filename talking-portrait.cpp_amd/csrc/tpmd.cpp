@@ -970,7 +970,7 @@ static TailArgs stage_tail_args(tpmd_ctx *c, int j, int n, float *img_dst) {
     a.s_next = last ? nullptr : c->L->s_all + c->conv[3 + 2 * j].s_off;
     a.trunk = last ? nullptr : c->L->trunk;
     a.warp_tap = nullptr;
-    a.featg = a.trunk ? nullptr : s.featg;
+    a.featg = s.featg;
     a.nframes = n;
     a.r = 8 << j;
     a.C = c->oc[j];
@@ -1725,7 +1725,7 @@ static int tpmd_stage_tail_body(tpmd_ctx *c, int j, const float *out, int n, con
     a.s_next = nullptr;
     a.trunk = trunk;
     a.warp_tap = warp;
-    a.featg = trunk || warp ? nullptr : s.featg;
+    a.featg = s.featg;
     a.nframes = n;
     a.r = 8 << j;
     a.C = c->oc[j];
@@ -1781,7 +1781,7 @@ static int tpmd_stage_conv_tail_body(tpmd_ctx *c, int j, const float *c1, int n,
     a.rgb_cur = rgb;
     a.trunk = trunk;
     a.warp_tap = warp;
-    a.featg = trunk || warp ? nullptr : c->st[j].featg;
+    a.featg = c->st[j].featg;
     a.nframes = n;
     a.r = r;
     a.C = C;

@@ -51,8 +51,9 @@ struct TailArgs {
     void *trunk;              // CL [frame][r*r][C] (TT) or null
     float *warp_tap;          // CL [frame][r*r][C] f32 or null (tests)
     // [r*r][4] f32: ToRGB weight . feat of each feature pixel (4th value 0),
-    // then TAIL_FEATG_PAD zero bytes; set only when neither trunk nor
-    // warp_tap is stored, so the warp is needed for the ToRGB sum alone
+    // then TAIL_FEATG_PAD zero bytes, or null; when set, the fused tile
+    // tails take the ToRGB sum from it instead of from the warp (the
+    // standalone per-pixel tail always sums the warp)
     const float *featg;
     int nframes, r, C;
 };

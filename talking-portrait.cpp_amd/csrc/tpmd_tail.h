@@ -181,7 +181,12 @@ namespace tpmd {
 //     Wf * s_f of the tile's frame are staged in LDS), flow skip, flow head,
 //     bilinear tap geometry; the per-pixel results go to LDS;
 //   phase 2, G = C/8 lanes per pixel: gather of the feature taps, warp,
-//     trunk (* next style, stored), ToRGB with a butterfly over the G lanes.
+//     trunk (* next style, stored).
+// The ToRGB sum is Wr . (m * sum_k w_k feat_k) = m * sum_k w_k (Wr . feat_k)
+// from the per-feature-pixel Wr . feat (TailArgs::featg), taken in phase 1:
+// 3 values per tap instead of C channels and a butterfly over the G lanes,
+// the ToRGB dot of phase 2 (measured at r256, 16 frames: 174 -> 167 us);
+// phase 2 then runs only for the trunk or the warp tap.
 // Per-pixel scalar work runs once instead of on each of the G lanes.  The
 // flow / rgb skips do not depend on the conv output: tile_tail_skips loads
 // them before the conv runs, so their latency hides behind it.
@@ -346,24 +351,27 @@ __device__ __forceinline__ void tail_flow_head(const TailArgs &a, float fl[3], i
     t = gather_geometry(gx, gy, r, r);
 }
 
-// part 2 when the warp feeds ToRGB alone (featg set): Wr . (m * sum_k w_k
-// feat_k) = m * sum_k w_k (Wr . feat_k), with Wr . feat stored per feature
-// pixel; a tap outside the map reads the zero pad after it
-__device__ __forceinline__ void tail_featg_rgb(const TailArgs &a, const taps4 &t, float m, int fr, int pix,
-                                               const tail_skip &sk) {
-#pragma clang fp contract(off)
+// the ToRGB sum from featg: Wr . (m * sum_k w_k feat_k) = m * sum_k w_k
+// (Wr . feat_k), with Wr . feat stored per feature pixel; a tap outside the
+// map reads the zero pad after it.  Load the four taps' values ...
+__device__ __forceinline__ void tail_featg_load(const TailArgs &a, const taps4 &t, floatx4 gv[4]) {
     const int r = a.r, RR = r * r;
     const char *gb = (const char *) a.featg;
     const unsigned gpad = (unsigned) RR * 16u;
     const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) t.x0 + 1u < (unsigned) r};
     const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) t.y0 + 1u < (unsigned) r};
     const unsigned base = (unsigned) (t.y0 * r + t.x0) * 16u;
-    floatx4 gv[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * 16);
         gv[k] = *(const floatx4 *) (gb + (inx[k & 1] && iny[k >> 1] ? off : gpad));
     }
+}
+// ... then form and store the pixel's rgb
+__device__ __forceinline__ void tail_featg_finish(const TailArgs &a, const taps4 &t, float m, int fr, int pix,
+                                                  const float skr[3], const floatx4 gv[4]) {
+#pragma clang fp contract(off)
+    const int RR = a.r * a.r;
     float rgb[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -376,11 +384,28 @@ __device__ __forceinline__ void tail_featg_rgb(const TailArgs &a, const taps4 &t
     for (int q = 0; q < 3; q++) {
         float v = leaky(rgb[q] * m + a.rlb[q]);
         v = v + a.rbias[q];
-        if (a.rgb_prev) v = v + sk.rgb[q];
+        if (a.rgb_prev) v = v + skr[q];
         rgbf[(unsigned) (q * RR + pix)] = v;
     }
 }
+__device__ __forceinline__ void tail_featg_rgb(const TailArgs &a, const taps4 &t, float m, int fr, int pix,
+                                               const tail_skip &sk) {
+    floatx4 gv[4];
+    tail_featg_load(a, t, gv);
+    tail_featg_finish(a, t, m, fr, pix, sk.rgb, gv);
+}
 
+// s_waitcnt immediate: lgkmcnt(0), vmcnt and expcnt not waited on
+constexpr int tail_waitcnt_lgkm0 = 0xF | (0x7 << 4) | (0x3 << 14);
+// the fused tile tail's phase 2: pixels whose feature taps are requested
+// together (f16 / f32 features), and whether the featg values of phase 1's
+// pixels stay in flight through phase 2
+constexpr int TAIL_NB16 = 4, TAIL_NB32 = 2;
+constexpr bool TAIL_FEATG_OVERLAP = false;
+
+// Runs after the activated tile `so` ([BN][SOS] f32) and `wfs` are written
+// and a barrier has made them visible; prm is [BN][PRM] scratch.  a.featg
+// must be set: the ToRGB sum is taken from it in phase 1.
 template <typename TF, typename TT, int C, int BN, int NT, int TWC>
 __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, float *prm, const float *wfs,
                                           int n0, int tid, const tail_skip &sk) {
@@ -394,8 +419,13 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     const int RR = r * r;
     const int fr = n0 / RR;                          // the tile lies in one frame
     const int pix0 = n0 - fr * RR;
+    // phase 2 gathers the warp channel by channel, for the trunk or the warp tap
+    const bool p2 = a.trunk || a.warp_tap;
 
     // ---- phase 1: one thread per pixel
+    taps4 gt{};
+    float gm = 0.0f;
+    floatx4 gv[4];
     if (tid < BN) {
         const int p = tid;
         const int pix = tile_pix<TWC>(pix0, r, p);
@@ -425,28 +455,38 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
         taps4 t;
         float m;
         tail_flow_head(a, fl, fr, pix, sk, t, m);
-        if (a.featg) {
-            tail_featg_rgb(a, t, m, fr, pix, sk);
+        if (p2) *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
+        if (p2) prm[p * L::PRM + 4] = m;
+        if (TAIL_FEATG_OVERLAP && p2) {
+            tail_featg_load(a, t, gv);
+            gt = t;
+            gm = m;
         } else {
-            *(floatx4 *) (prm + p * L::PRM) = floatx4{__int_as_float(t.x0), __int_as_float(t.y0), t.wx, t.wy};
-            *(floatx4 *) (prm + p * L::PRM + 4) = floatx4{m, sk.rgb[0], sk.rgb[1], sk.rgb[2]};
+            tail_featg_rgb(a, t, m, fr, pix, sk);
         }
     }
-    if (a.featg) return;  // (uniform) nothing is left for phase 2
-    __syncthreads();
+    if (!p2) return;  // (uniform) nothing is left for phase 2
+    if constexpr (TAIL_FEATG_OVERLAP) {
+        // the records are in LDS for every wave; a bare barrier, so the
+        // featg loads stay in flight
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(tail_waitcnt_lgkm0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    } else {
+        __syncthreads();
+    }
 
     // ---- phase 2: G lanes per pixel, 8 channels each; the feature taps of
     // NB pixels are requested together, then used
     constexpr int ITER = BN / PPB;
-    constexpr int NBMAX = sizeof(TF) == 2 ? 4 : 2;
+    constexpr int NBMAX = sizeof(TF) == 2 ? TAIL_NB16 : TAIL_NB32;
     constexpr int NB = ITER < NBMAX ? ITER : NBMAX;
     static_assert(ITER % NB == 0, "tail batch");
     const int lane = tid & 63, wid = tid >> 6;
     const int gl = lane % G, grp = lane / G;
     const int c0 = gl * 8;
-    float wr[3][8], sn[8];
-#pragma unroll
-    for (int k = 0; k < 3; k++) load8<float>::run(a.wrgb + k * C + c0, wr[k]);
+    float sn[8];
     if (a.s_next) load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
     // 32-bit byte offsets from per-frame bases; a tap outside the map reads
     // the zero pad that follows the feature map (TAIL_FEAT_PAD bytes), whose
@@ -455,7 +495,6 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     const unsigned pad_off = (unsigned) RR * C * (unsigned) sizeof(TF);
     char *trunkb = a.trunk ? (char *) a.trunk + (int64_t) fr * RR * C * (int64_t) sizeof(TT) : nullptr;
     float *warpf = a.warp_tap ? a.warp_tap + (int64_t) fr * RR * C : nullptr;
-    float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
     for (int it0 = 0; it0 < ITER; it0 += NB) {
         taps4 t[NB];
         float m[NB];
@@ -498,7 +537,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
             for (int e = 0; e < 8; e++) warp[e] = smp[e] * m[b];
             const unsigned po = (unsigned) pix * C + c0;
             if (warpf) store8<float>(warpf + po, warp);
-            if (trunkb) {  // the last stage has no trunk: the conv output is not read again
+            if (trunkb) {
                 const floatx4 x0 = *(const floatx4 *) (so + lp * L::SOS + c0);
                 const floatx4 x1 = *(const floatx4 *) (so + lp * L::SOS + c0 + 4);
                 const float ov[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
@@ -512,23 +551,11 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
                 }
                 store8<TT>((TT *) (trunkb + po * (unsigned) sizeof(TT)), trunk);
             }
-            float rgb[3];
-#pragma unroll
-            for (int k = 0; k < 3; k++) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc = __builtin_fmaf(wr[k][e], warp[e], acc);
-                rgb[k] = group_sum<G>(acc);
-            }
-            if (gl < 3) {
-                const int k = gl;
-                const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
-                float v = leaky(rv + a.rlb[k]);
-                v = v + a.rbias[k];
-                if (a.rgb_prev) v = v + prm[lp * L::PRM + 5 + k];
-                rgbf[(unsigned) (k * RR + pix)] = v;
-            }
         }
+    }
+    if (TAIL_FEATG_OVERLAP && tid < BN) {
+        const float skr[3] = {sk.rgb[0], sk.rgb[1], sk.rgb[2]};
+        tail_featg_finish(a, gt, gm, fr, tile_pix<TWC>(pix0, r, tid), skr, gv);
     }
 }
 
