@@ -443,7 +443,7 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     }
     if (!fused && c.A_perm && modconv_hfrag_ok(c.f16, c.out_f16, c.mode, c.IC, c.OC, c.H, c.W)) {
         p.A = c.A_perm;
-        return launch_modconv_hfrag(p, c.mode, st);
+        return launch_modconv_hfrag(p, c.mode, c.out_f16, st);
     }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);

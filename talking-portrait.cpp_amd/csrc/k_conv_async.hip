@@ -447,42 +447,57 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
 }
 
 // ---------------------------------------------------------------------------
-// Halo up-conv / dense conv (f16 operands and output, every tile inside one
-// frame): a tile is 256 GEMM rows x an 8 x 32 block of pixels of one frame,
-// and the k order is channel-chunk major, k tile t = c*9 + tap (32 channels
-// c*32 .. +31 of tap `tap`).  Per chunk the 10 x 34 halo of those 32 channels
-// is fetched once into one of two LDS halo buffers (80-byte pixels: 4 chunks
-// of 8 channels + a pad chunk, so 32 consecutive pixels read at any offset
-// hit distinct banks), and its 9 taps read it shifted by (dy, dx): the B
-// bytes moved per chunk drop from 9 x 16 KB of im2col rows to one 27 KB halo.
-constexpr int HR_TH = 8, HR_TW = 32, HR_HWD = HR_TW + 2, HR_HPX = (HR_TH + 2) * HR_HWD;
-constexpr int HR_PXB = 80;              // halo pixel: 64 bytes of channels + 16-byte pad
-constexpr int HR_HBUF = 32 * 1024;      // one halo buffer: 32 units of 1 KB
-static_assert(HR_HPX * HR_PXB <= HR_HBUF, "halo buffer");
-
+// Halo convs (f16 operands, every tile inside one frame): a tile is BM GEMM
+// rows x a TH x TW block of pixels of one frame, and the k order is
+// channel-chunk major, k tile t = c*9 + tap (32 channels c*32 .. +31 of tap
+// `tap`).  Per chunk the (TH+2) x (TW+2) halo of those 32 channels sits in
+// one of two LDS halo buffers (80-byte pixels: 4 chunks of 8 channels + a pad
+// chunk, so 32 consecutive pixels read at any offset hit distinct banks), and
+// its 9 taps read it shifted by (dy, dx): the B bytes moved per chunk drop
+// from 9 x 16 KB of im2col rows to one halo of at most 32 KB.
+//
 // A is read by every wave straight from L2 in MFMA fragment order
-// (A_ORDER_FRAG: each fragment is one contiguous 1 KB), not through LDS.  Waves are 4 x 2 with 64 x 128 tiles, so a wave reads
-// 2 A fragments and 4 B fragments per 16-wide k step.  The two waves that
-// share A rows read the same lines, and the second finds them in L1.  The LDS
-// holds only the two halo buffers, so the one barrier per 32-channel chunk
-// (9 k tiles) is the halo hand-over; A needs no barrier.
+// (A_ORDER_FRAG: each fragment is one contiguous 1 KB), not through LDS.
+// Eight waves, each 64 rows x BN/WN pixels (WM = BM/64 wave rows, WN = 8/WM
+// wave columns): per 16-wide k step a wave reads 2 A fragments and TN B
+// fragments for 2*TN MFMAs.  The waves that share A rows read the same lines
+// and find them in L1.  The LDS holds only the two halo buffers, so the one
+// barrier per 32-channel chunk (9 k tiles) is the halo hand-over; A needs no
+// barrier.
 //   * A fragments are requested two k tiles ahead into three register sets
 //     (k tile t in set t % 3; 9 taps per chunk keep the set of a tap fixed);
 //   * the B fragments of the next k step are read from LDS while the
 //     current step's MFMAs run;
 //   * the halo of chunk c+1 is loaded into registers early in chunk c and
 //     written to the other LDS buffer late in it; one barrier ends the chunk.
-template <int MODE, int NC>
+// Configurations (hfrag_config): 256 rows x 8 x 32 pixels (the r64 - r256
+// up-convs); 128 rows x 8 x 32 or x 16 x 16 pixels where 256 rows leave fewer
+// than 256 tiles at 16 frames (the r32 convs: a 32 x 32 map, a 16 x 16 up-conv
+// input).  The output goes through an LDS stage ([pixel][row], f16 or f32)
+// and is written as whole 16-byte chunks of contiguous memory.
+constexpr int HR_PXB = 80;              // halo pixel: 64 bytes of channels + 16-byte pad
+constexpr int HR_HBUF = 32 * 1024;      // one halo buffer: 32 units of 1 KB per wave-set
+
+template <int BM_, int TH_, int TW_>
+struct hfrag_cfg {
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, BN = TH * TW;
+    static constexpr int NW = 8, NT = NW * 64;
+    static constexpr int WM = BM / 64, WN = NW / WM;    // wave grid
+    static constexpr int TM = 2, TN = BN / 32 / WN;      // 64 x 32*TN per wave
+    static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
+    static constexpr int LPH = HR_HBUF / 1024 / NW;      // halo units of 1 KB per wave per chunk
+    static_assert(WM * WN == NW && TN * 32 * WN == BN && BN == 256, "wave grid");
+    static_assert(HPX * HR_PXB <= HR_HBUF, "halo buffer");
+};
+
+template <int MODE, int NC, int BM, int TH, int TW, typename TO>
 __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int tiles_x, int tiles_frame) {
     typedef half_t TA;
-    constexpr int NW = 8, NT = NW * 64, WN = 2;
-    constexpr int BM = 256, BN = HR_TH * HR_TW;
-    constexpr int TM = 2, TN = 4;                        // 64 x 128 per wave
-    constexpr int LPH = HR_HBUF / 1024 / NW;             // halo DMA instructions per wave per chunk
-    constexpr int ORS = BM * 2 + 16, OUT = BN * ORS;     // staged f16 output, one padded row per pixel
+    typedef hfrag_cfg<BM, TH, TW> F;
+    constexpr int NW = F::NW, NT = F::NT, WN = F::WN, BN = F::BN, TM = F::TM, TN = F::TN;
+    constexpr int HWD = F::HWD, HPX = F::HPX, LPH = F::LPH;
+    constexpr int ORS = BM * (int) sizeof(TO) + 16, OUT = BN * ORS;  // staged output, one padded row per pixel
     constexpr int LDS = 2 * HR_HBUF > OUT ? 2 * HR_HBUF : OUT;
-    constexpr int A_PER_TILE = 2 * TM;                   // A loads per wave per k tile
-    static_assert(BM / 32 == 4 * TM && BN / 32 == WN * TN, "wave grid");
     __shared__ __attribute__((aligned(16))) char smem[LDS];
 
     const int tid = threadIdx.x;
@@ -493,7 +508,7 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     const int fr = nt / tiles_frame;
     const int trem = nt - fr * tiles_frame;
     const int ty = trem / tiles_x;
-    const int y0 = ty * HR_TH, x0 = (trem - ty * tiles_x) * HR_TW;
+    const int y0 = ty * TH, x0 = (trem - ty * tiles_x) * TW;
     const int m0 = mt * BM;
     constexpr int IC = NC * 32, KSA = IC / 16;
     const int H = p.H, W = p.W;
@@ -520,9 +535,9 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     for (int h = 0; h < LPH; h++) {
         const int u = (wid * LPH + h) * 64 + lane;
         const int hp = u / 5, q = u - hp * 5;
-        const int hy = hp / HR_HWD, hx = hp - hy * HR_HWD;
+        const int hy = hp / HWD, hx = hp - hy * HWD;
         const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-        hok[h] = q < 4 && hp < HR_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
+        hok[h] = q < 4 && hp < HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
         hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * IC + q * 8 : Xf;
     }
     // the halo goes through registers rather than the LDS DMA path: the
@@ -547,12 +562,17 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
 
     const int lrow = lane & 31, khalf = lane >> 5;
-    // this lane's halo pixel for tap (0, 0) of fragment b: block row TN*wn + b, column lrow
-    const int hbase = ((TN * wn) * HR_HWD + lrow) * HR_PXB + khalf * 16;
+    // this lane's halo pixel for tap (0, 0) of fragment b: block pixel
+    // (wn*TN + b)*32 + lrow
+    int hoff[TN];
+    static_for<TN>([&](auto b) {
+        const int n = (wn * TN + b) * 32 + lrow;
+        hoff[b] = ((n / TW) * HWD + n % TW) * HR_PXB + khalf * 16;
+    });
     auto read_b = [&](const char *hb, int tap, int s, u32x4 (&bf)[TN]) {
         const int dy = tap / 3, dx = tap - dy * 3;
-        const char *q = hb + (dy * HR_HWD + dx) * HR_PXB + s * 32;
-        static_for<TN>([&](auto b) { bf[b] = *(const u32x4 *) (q + b * HR_HWD * HR_PXB); });
+        const char *q = hb + (dy * HWD + dx) * HR_PXB + s * 32;
+        static_for<TN>([&](auto b) { bf[b] = *(const u32x4 *) (q + hoff[b]); });
     };
 
     load_h(0);
@@ -564,7 +584,7 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     // memory-counter waits are exact: no wait drains the loads in flight
     static_for<NC>([&](auto cc) {
         constexpr int c = decltype(cc)::value;
-        const char *hb = smem + hbase + (c & 1) * HR_HBUF;
+        const char *hb = smem + (c & 1) * HR_HBUF;
         u32x4 bcur[TN];
         read_b(hb, 0, 0, bcur);
         static_for<18>([&](auto q) {
@@ -591,7 +611,7 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
         if constexpr (c + 1 < NC) __syncthreads();   // halo c+1 written, chunk c's reads done
     });
 
-    // f16 store epilogue: the tile is staged in LDS as [pixel][row] (528-byte
+    // store epilogue: the tile is staged in LDS as [pixel][row] (ORS-byte
     // rows) and written back as whole 16-byte chunks of contiguous output
     __syncthreads();
     static_for<TN>([&](auto b) {
@@ -605,32 +625,39 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
                 const floatx4 bb = *(const floatx4 *) (p.bias + o);
                 floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
                 if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
-                half4 hv;
+                floatx4 v;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    float v = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
-                    if (p.out_scale) v *= sc[j];
-                    hv[j] = (half_t) v;
+                    v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                    if (p.out_scale) v[j] *= sc[j];
                 }
-                *(half4 *) (smem + nl * ORS + ml * 2) = hv;
+                if constexpr (sizeof(TO) == 2) {
+                    half4 hv;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) hv[j] = (half_t) v[j];
+                    *(half4 *) (smem + nl * ORS + ml * 2) = hv;
+                } else {
+                    *(floatx4 *) (smem + nl * ORS + ml * 4) = v;
+                }
             });
         });
     });
     __syncthreads();
-    constexpr int CPR = BM / 8, NCH = BN * CPR, STEP = NT / CPR;
-    static_assert(NCH % NT == 0 && NT % CPR == 0 && HR_TW % STEP == 0, "store pass");
+    constexpr int EPC = 16 / (int) sizeof(TO);           // output elements per 16-byte chunk
+    constexpr int CPR = BM / EPC, NCH = BN * CPR, STEP = NT / CPR;
+    static_assert(NCH % NT == 0 && NT % CPR == 0, "store pass");
     const int mc = tid % CPR;
-    const int m = m0 + mc * 8;
+    const int m = m0 + mc * EPC;
     int cls = 0, o = m;
     if constexpr (MODE == MODE_SUBPIX) {
         cls = m / p.OC;
         o = m - cls * p.OC;
     }
     const int64_t HW = (int64_t) H * W;
-    half_t *Yp = (half_t *) p.Y;
+    TO *Yp = (TO *) p.Y;
     static_for<NCH / NT>([&](auto j) {
         const int nl = tid / CPR + j * STEP;
-        const int y = y0 + nl / HR_TW, x = x0 + nl % HR_TW;
+        const int y = y0 + nl / TW, x = x0 + nl % TW;
         int64_t opix;
         if constexpr (MODE == MODE_DENSE) opix = fr * HW + (int64_t) y * W + x;
         else opix = fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
@@ -639,40 +666,72 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_kernel(ConvParams p, int
     });
 }
 
-// the 256-row halo kernel: f16 operands and output, M a multiple of 256, IC a
-// power of two from 32 to 512, input maps of 8 x 32 blocks, and enough tiles
-// at 16 frames to give every CU one
-bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
-    const int M = mode == MODE_DENSE ? OC : 4 * OC;
-    if (!f16 || !out_f16 || M % 256 != 0 || H % HR_TH != 0 || W % HR_TW != 0) return false;
-    if (IC != 32 && IC != 64 && IC != 128 && IC != 256 && IC != 512) return false;
-    return (int64_t) (M / 256) * 16 * (H / HR_TH) * (W / HR_TW) >= 256;
+// the halo kernel configuration of a conv shape: 1 = 256 rows x 8 x 32
+// pixels, 2 = 128 rows x 8 x 32, 3 = 128 rows x 16 x 16, 0 = none.  f16
+// operands, IC a power of two from 32 to 512, and the first configuration
+// (in that order) that gives every CU a tile at 16 frames; a function of the
+// per-frame shape only
+static int hfrag_config(bool f16, int mode, int IC, int H, int W, int M) {
+    if (!f16 || (IC != 32 && IC != 64 && IC != 128 && IC != 256 && IC != 512)) return 0;
+    auto tiles = [&](int bm, int th, int tw) -> int64_t {
+        if (M % bm != 0 || H % th != 0 || W % tw != 0) return 0;
+        return (int64_t) (M / bm) * 16 * (H / th) * (W / tw);
+    };
+    if (tiles(256, 8, 32) >= 256) return 1;
+    if (tiles(128, 8, 32) >= 256) return 2;
+    if (tiles(128, 16, 16) >= 256) return 3;
+    return 0;
 }
 
-hipError_t launch_modconv_hfrag(ConvParams p, int mode, hipStream_t st) {
-    if (p.M % 256 != 0 || p.H % HR_TH != 0 || p.W % HR_TW != 0) return hipErrorInvalidValue;
+// f16 output, or f32 output of a dense conv on 128-row tiles
+bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
+    const int M = mode == MODE_DENSE ? OC : 4 * OC;
+    const int cfg = hfrag_config(f16, mode, IC, H, W, M);
+    return cfg != 0 && (out_f16 || (mode == MODE_DENSE && cfg != 1));
+}
+
+hipError_t launch_modconv_hfrag(ConvParams p, int mode, bool out_f16, hipStream_t st) {
+    const int cfg = hfrag_config(true, mode, p.IC, p.H, p.W, p.M);
+    if (cfg == 0 || (!out_f16 && (mode != MODE_DENSE || cfg == 1))) return hipErrorInvalidValue;
+    const int BM = cfg == 1 ? 256 : 128, TH = cfg == 3 ? 16 : 8, TW = cfg == 3 ? 16 : 32;
     const int64_t HW = (int64_t) p.H * p.W;
     if (p.N % HW != 0) return hipErrorInvalidValue;
-    p.MT = p.M / 256;
+    p.MT = p.M / BM;
     p.T = 9 * p.IC / 32;
-    const int tiles_x = p.W / HR_TW, tiles_frame = tiles_x * (p.H / HR_TH);
-    const int64_t tiles = (int64_t) p.MT * (p.N / HW) * tiles_frame;
-    auto go = [&](auto nc) {
-        constexpr int NC = decltype(nc)::value;
-        if (mode == MODE_DENSE)
-            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC>), dim3((unsigned) tiles), dim3(512), 0, st, p,
-                               tiles_x, tiles_frame);
+    const int tiles_x = p.W / TW, tiles_frame = tiles_x * (p.H / TH);
+    const dim3 grid((unsigned) ((int64_t) p.MT * (p.N / HW) * tiles_frame));
+    auto go = [&](auto nc, auto bm, auto th, auto tw) {
+        constexpr int NC = decltype(nc)::value, B = decltype(bm)::value;
+        constexpr int T_H = decltype(th)::value, T_W = decltype(tw)::value;
+        if (mode == MODE_SUBPIX)
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC, B, T_H, T_W, half_t>), grid, dim3(512), 0,
+                               st, p, tiles_x, tiles_frame);
+        else if (out_f16)
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC, B, T_H, T_W, half_t>), grid, dim3(512), 0,
+                               st, p, tiles_x, tiles_frame);
+        else if constexpr (B == 128)   // a 256-row f32 stage would not fit the LDS
+            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC, B, T_H, T_W, float>), grid, dim3(512), 0,
+                               st, p, tiles_x, tiles_frame);
         else
-            hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC>), dim3((unsigned) tiles), dim3(512), 0, st,
-                               p, tiles_x, tiles_frame);
+            return hipErrorInvalidValue;
         return hipGetLastError();
     };
+    auto by_cfg = [&](auto nc) {
+        if (cfg == 1)
+            return go(nc, std::integral_constant<int, 256>{}, std::integral_constant<int, 8>{},
+                      std::integral_constant<int, 32>{});
+        if (cfg == 2)
+            return go(nc, std::integral_constant<int, 128>{}, std::integral_constant<int, 8>{},
+                      std::integral_constant<int, 32>{});
+        return go(nc, std::integral_constant<int, 128>{}, std::integral_constant<int, 16>{},
+                  std::integral_constant<int, 16>{});
+    };
     switch (p.IC) {
-        case 32: return go(std::integral_constant<int, 1>{});
-        case 64: return go(std::integral_constant<int, 2>{});
-        case 128: return go(std::integral_constant<int, 4>{});
-        case 256: return go(std::integral_constant<int, 8>{});
-        case 512: return go(std::integral_constant<int, 16>{});
+        case 32: return by_cfg(std::integral_constant<int, 1>{});
+        case 64: return by_cfg(std::integral_constant<int, 2>{});
+        case 128: return by_cfg(std::integral_constant<int, 4>{});
+        case 256: return by_cfg(std::integral_constant<int, 8>{});
+        case 512: return by_cfg(std::integral_constant<int, 16>{});
         default: return hipErrorInvalidValue;
     }
 }

@@ -120,10 +120,11 @@ hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nspl
 // k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128,
 // 256} (tiles of 256, 128, 128, 128 pixels of one frame) with the same ring
 bool modconv_tail_async_ok(int OC, int r);
-// 256-row tiles over 8 x 32 pixel blocks with the input halo in LDS and A
-// read from L2 in fragment order (k_conv_async.hip, A_ORDER_FRAG)
+// 256- or 128-row tiles over 8 x 32 or 16 x 16 pixel blocks with the input
+// halo in LDS and A read from L2 in fragment order (k_conv_async.hip,
+// A_ORDER_FRAG); f16 output, or f32 output of a dense conv
 bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
-hipError_t launch_modconv_hfrag(ConvParams p, int mode, hipStream_t st);
+hipError_t launch_modconv_hfrag(ConvParams p, int mode, bool out_f16, hipStream_t st);
 // k_conv_up.hip: f16 composed sub-pixel up-conv 64 -> 32 channels with f16
 // output, on 4 x 32 halo tiles (H % 4 == 0, W % 32 == 0)
 bool modconv_up64_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
