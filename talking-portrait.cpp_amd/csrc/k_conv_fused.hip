@@ -32,7 +32,11 @@ namespace tpmd {
 // three per CU, 222 us; the same with F32_SWZ (four per CU) 184 us;
 // 16 x 32 blocks of 8 waves (two per CU: A loaded once per 512 pixels, 18
 // halo rows per 16) 175 us, 183 us with F32_SWZ.  The non-FG form keeps the
-// same blocks (its activated tile takes 90 KB of LDS: one per CU).
+// same blocks (its activated tile takes 90 KB of LDS: one per CU).  A
+// persistent form (each workgroup walking a run of tiles, A loaded once, the
+// next tile's halo, skips and ToFlow weights requested under the current
+// tile's conv) needs 200+ registers, two waves per SIMD: 213-221 us against
+// 171; capped at four waves per SIMD it spills (531 us).
 constexpr int F32_NT = 512;
 constexpr bool F32_SWZ = false;
 

@@ -40,8 +40,15 @@ struct up64_cfg {
     static_assert(OCH % NT == 0, "store pass");
 };
 
+// Four waves per SIMD (128 registers: the accumulators in VGPRs, no AGPRs),
+// so four workgroups share a CU, as many as its LDS holds: measured at 16
+// frames 178 -> 163 us against three per SIMD (160 registers).  Two waves of
+// two classes each (each B fragment read from LDS feeding two MFMAs, 204
+// registers, two waves per SIMD) measured no faster than three per SIMD.
 template <int TH, bool FRAG>
-__global__ __launch_bounds__(256) void upconv64_kernel(ConvParams p, int tiles_x, int tiles_frame) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void upconv64_kernel(ConvParams p,
+                                                                                             int tiles_x,
+                                                                                             int tiles_frame) {
     typedef half_t TA;
     typedef up64_cfg<TH> F;
     constexpr int IC = F::IC, OC = F::OC, NT = F::NT, TW = F::TW, HWD = F::HWD, PXB = F::PXB;
@@ -146,134 +153,8 @@ __global__ __launch_bounds__(256) void upconv64_kernel(ConvParams p, int tiles_x
     });
 }
 
-// ---------------------------------------------------------------------------
-// The same up-conv with two waves per workgroup, wave w computing the two
-// parity classes 2w, 2w+1 (GEMM rows 64w .. 64w+63) for every pixel of the
-// block: per 16-wide k step a wave reads 2 A fragments (L2) and TH B
-// fragments (LDS) for 2*TH MFMAs, so each B fragment read from LDS feeds
-// two MFMAs instead of one (the four-wave form reads every halo fragment
-// once per class, which keeps the LDS as busy as the MFMA pipe).  128
-// accumulator registers per lane: two waves per SIMD.  A fragments are
-// requested PFT taps ahead.  Same products in the same order as
-// upconv64_kernel, so the frames are the same bits.
-template <int TH, int PFT>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void upconv64w2_kernel(ConvParams p, int tiles_x, int tiles_frame) {
-    typedef half_t TA;
-    typedef up64_cfg<TH> F;
-    constexpr int IC = F::IC, OC = F::OC, TW = F::TW, HWD = F::HWD, PXB = F::PXB;
-    constexpr int CPP = F::CPP, HCH = F::HCH, KS = F::KS, OPX = F::OPX, OPB = F::OPB;
-    constexpr int NT = 128, PF = (HCH + NT - 1) / NT;
-    constexpr int NS = PFT + 1;                    // A register sets
-    static_assert(F::OCH % NT == 0, "store pass");
-    __shared__ __attribute__((aligned(16))) char smem[F::LDS];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wid = tid >> 6;
-    const int lrow = lane & 31, khalf = lane >> 5;
-    const int tile = xcd_remap((int) blockIdx.x, (int) gridDim.x);
-    const int fr = tile / tiles_frame;
-    const int trem = tile - fr * tiles_frame;
-    const int ty = trem / tiles_x, tx = trem - ty * tiles_x;
-    const int H = p.H, W = p.W;
-    const int y0 = ty * TH, x0 = tx * TW;
-
-    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
-    u32x4 hv[PF];
-    static_for<PF>([&](auto i) {
-        const int ch = tid + i * NT;
-        hv[i] = u32x4{0u, 0u, 0u, 0u};
-        if (ch < HCH) {
-            const int px = ch / CPP, c = ch - px * CPP;
-            const int hy = px / HWD, hx = px - hy * HWD;
-            const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-            if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
-                hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * IC + c * 8);
-        }
-    });
-    // A in fragment order: fragment (tap, step) of row block (class) c is
-    // 1 KB at ((tap*KS + step)*4 + c) KB; classes 2*wid and 2*wid+1
-    const TA *arow = (const TA *) p.A + (wid * 128 + lane) * 8;
-    auto afrag = [&](int tap, int s, int a) -> u32x4 {
-        return *(const u32x4 *) (arow + ((tap * KS + s) * 4 + a) * 512);
-    };
-    u32x4 af[NS][2][KS];   // tap t's fragments in set t % NS, requested PFT taps ahead
-    static_for<PFT>([&](auto t) {
-        static_for<KS>([&](auto s) { static_for<2>([&](auto a) { af[t][a][s] = afrag(t, s, a); }); });
-    });
-    static_for<PF>([&](auto i) {
-        const int ch = tid + i * NT;
-        if (ch < HCH) {
-            const int px = ch / CPP, c = ch - px * CPP;
-            *(u32x4 *) (smem + px * PXB + c * 16) = hv[i];
-        }
-    });
-    __syncthreads();
-
-    floatx16 acc[2][TH];
-    static_for<2>([&](auto a) {
-        static_for<TH>([&](auto b) {
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
-        });
-    });
-    static_for<9>([&](auto tap) {
-        constexpr int dy = tap / 3, dx = tap % 3;
-        constexpr int cur = tap % NS;
-        if constexpr (tap + PFT < 9)
-            static_for<KS>([&](auto s) {
-                static_for<2>([&](auto a) { af[(tap + PFT) % NS][a][s] = afrag(tap + PFT, s, a); });
-            });
-        static_for<KS>([&](auto s) {
-            static_for<TH>([&](auto b) {
-                const u32x4 bf =
-                    *(const u32x4 *) (smem + ((b + dy) * HWD + lrow + dx) * PXB + (s * 2 + khalf) * 16);
-                mfma_op<TA>::run(af[cur][0][s], bf, acc[0][b]);
-                mfma_op<TA>::run(af[cur][1][s], bf, acc[1][b]);
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    });
-    __syncthreads();
-
-    // epilogue: class (by, bx) = (wid, a) of low-res pixel (y0+b, x0+lrow) is
-    // output pixel (2(y0+b)+by, 2(x0+lrow)+bx); channels i*8 + khalf*4 .. +4
-    const int by = wid;
-    static_for<4>([&](auto i) {
-        const int o = i * 8 + khalf * 4;
-        const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * OC + o);
-        const floatx4 bb = *(const floatx4 *) (p.bias + o);
-        floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
-        if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * OC + o);
-        static_for<2>([&](auto a) {
-            static_for<TH>([&](auto b) {
-                half4 h;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float v = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
-                    if (p.out_scale) v *= sc[j];
-                    h[j] = (half_t) v;
-                }
-                *(half4 *) (smem + ((2 * b + by) * OPX + 2 * lrow + (int) a) * OPB + o * 2) = h;
-            });
-        });
-    });
-    __syncthreads();
-
-    half_t *Yf = (half_t *) p.Y + (int64_t) fr * 4 * H * W * OC;
-    static_for<F::OCH / NT>([&](auto j) {
-        const int c = tid + j * NT;
-        const int row = c / (OPX * 4), rem = c - row * (OPX * 4);
-        const int px = rem >> 2, part = rem & 3;
-        const u32x4 v = *(const u32x4 *) (smem + (row * OPX + px) * OPB + part * 16);
-        *(u32x4 *) (Yf + ((int64_t) (2 * y0 + row) * (2 * W) + 2 * x0 + px) * OC + part * 8) = v;
-    });
-}
-
-// block rows: 4 keeps the accumulators at 64 registers (three waves per SIMD)
+// block rows: 4 keeps the accumulators at 64 registers
 constexpr int UP64_TH = 4;
-// the two-wave form (A fragment order only), and its A prefetch distance
-constexpr bool UP64_W2 = true;
-constexpr int UP64_W2_PFT = 1;
 
 bool modconv_up64_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
     return f16 && out_f16 && mode == MODE_SUBPIX && IC == 64 && OC == 32 && W % 32 == 0 && H % UP64_TH == 0;
@@ -284,10 +165,7 @@ hipError_t launch_modconv_up64(const ConvParams &p, bool frag, hipStream_t st) {
     if (p.IC != 64 || p.OC != 32 || p.M != 128 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
-    if (frag && UP64_W2)
-        hipLaunchKernelGGL((upconv64w2_kernel<TH, UP64_W2_PFT>), dim3((unsigned) (nframes * tiles_frame)), dim3(128),
-                           0, st, p, tiles_x, tiles_frame);
-    else if (frag)
+    if (frag)
         hipLaunchKernelGGL((upconv64_kernel<TH, true>), dim3((unsigned) (nframes * tiles_frame)), dim3(256), 0, st,
                            p, tiles_x, tiles_frame);
     else
