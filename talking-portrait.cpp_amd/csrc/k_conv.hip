@@ -305,6 +305,8 @@ int modconv_a_order(bool f16, bool out_f16, int mode, int IC, int OC, int H, int
     if (mode == MODE_DENSE && H == W && modconv_fusable(OC, H, f16) &&
         (modconv_fused32_ok(f16, IC, OC, H) || modconv_fused64_ok(f16, IC, OC, H)))
         return A_ORDER_FRAG;
+    if (mode == MODE_DENSE && H == W && modconv_fusable(OC, H, f16) && modconv_hfrag_tail_ok(f16, IC, OC, H, W))
+        return A_ORDER_FRAG;
     if (mode == MODE_DENSE && H == W && f16 && OC == 256 && IC % 32 == 0 && modconv_fusable(OC, H, f16))
         return A_ORDER_RING_TAP;
     if (modconv_hfrag_ok(f16, out_f16, mode, IC, OC, H, W)) return A_ORDER_FRAG;
@@ -454,6 +456,10 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (fused && modconv_fused64_ok(c.f16, c.IC, c.OC, c.H)) {
         if (c.A_perm) p.A = c.A_perm;
         return launch_modconv_fused64(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
+    }
+    if (fused && c.A_perm && modconv_hfrag_tail_ok(c.f16, c.IC, c.OC, c.H, c.W)) {
+        p.A = c.A_perm;
+        return launch_modconv_hfrag_tail(p, *c.tail, c.trunk_f16, st);
     }
     if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H)) {
         if (c.A_perm && c.OC == 256) {
