@@ -449,6 +449,10 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     }
     if (modconv_halo_ok(c.f16, c.mode, c.IC, c.OC, c.H, c.W, fused))
         return launch_modconv_halo(p, c.mode, c.out_f16, st);
+    if (fused && c.A_perm && modconv_hfrag_tail_ok(c.f16, c.IC, c.OC, c.H, c.W)) {
+        p.A = c.A_perm;
+        return launch_modconv_hfrag_tail(p, *c.tail, c.trunk_f16, st);
+    }
     if (fused && modconv_fused32_ok(c.f16, c.IC, c.OC, c.H)) {
         if (c.A_perm) p.A = c.A_perm;
         return launch_modconv_fused32(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
@@ -456,10 +460,6 @@ hipError_t launch_modconv(const ConvArgs &c, hipStream_t st) {
     if (fused && modconv_fused64_ok(c.f16, c.IC, c.OC, c.H)) {
         if (c.A_perm) p.A = c.A_perm;
         return launch_modconv_fused64(p, *c.tail, c.trunk_f16, c.A_perm != nullptr, st);
-    }
-    if (fused && c.A_perm && modconv_hfrag_tail_ok(c.f16, c.IC, c.OC, c.H, c.W)) {
-        p.A = c.A_perm;
-        return launch_modconv_hfrag_tail(p, *c.tail, c.trunk_f16, st);
     }
     if (fused && c.f16 && c.IC % 32 == 0 && modconv_tail_async_ok(c.OC, c.H)) {
         if (c.A_perm && c.OC == 256) {

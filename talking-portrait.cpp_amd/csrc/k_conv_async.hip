@@ -478,7 +478,7 @@ __global__ __launch_bounds__(WM *WN * 64) void modconv3x3_tail_async_kernel(Conv
 constexpr int HR_PXB = 80;              // halo pixel: 64 bytes of channels + 16-byte pad
 constexpr int HR_HBUF = 32 * 1024;      // one halo buffer: 32 units of 1 KB per wave-set
 // the C = 256 dense conv + tail on the halo conv (else on the im2col ring)
-constexpr bool HFRAG_TAIL = true;
+constexpr bool HFRAG_TAIL = true, HFRAG_TAIL128 = true;
 
 template <int BM_, int TH_, int TW_>
 struct hfrag_cfg {
@@ -822,21 +822,27 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_tail_kernel(ConvParams p
 }
 
 bool modconv_hfrag_tail_ok(bool f16, int IC, int OC, int H, int W) {
-    return HFRAG_TAIL && f16 && IC == 256 && OC == 256 && H % HT_TH == 0 && W % HT_TW == 0;
+    return HFRAG_TAIL && f16 && IC == OC && (OC == 256 || (OC == 128 && HFRAG_TAIL128)) && H % HT_TH == 0 &&
+           W % HT_TW == 0;
 }
 
 hipError_t launch_modconv_hfrag_tail(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st) {
-    if (p.IC != 256 || p.OC != 256 || p.M != 256 || p.H % HT_TH != 0 || p.W % HT_TW != 0)
+    if (p.IC != p.OC || (p.OC != 256 && p.OC != 128) || p.M != p.OC || p.H % HT_TH != 0 || p.W % HT_TW != 0)
         return hipErrorInvalidValue;
     const int tiles_x = p.W / HT_TW, tiles_frame = tiles_x * (p.H / HT_TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
-    if (trunk_f16)
-        hipLaunchKernelGGL((modconv3x3_hfrag_tail_kernel<half_t, half_t, 256>), grid, dim3(512), 0, st, p, ta,
-                           tiles_x, tiles_frame);
-    else
-        hipLaunchKernelGGL((modconv3x3_hfrag_tail_kernel<half_t, float, 256>), grid, dim3(512), 0, st, p, ta,
-                           tiles_x, tiles_frame);
+    auto go = [&](auto c) {
+        constexpr int CC = decltype(c)::value;
+        if (trunk_f16)
+            hipLaunchKernelGGL((modconv3x3_hfrag_tail_kernel<half_t, half_t, CC>), grid, dim3(512), 0, st, p, ta,
+                               tiles_x, tiles_frame);
+        else
+            hipLaunchKernelGGL((modconv3x3_hfrag_tail_kernel<half_t, float, CC>), grid, dim3(512), 0, st, p, ta,
+                               tiles_x, tiles_frame);
+    };
+    if (p.OC == 256) go(std::integral_constant<int, 256>{});
+    else go(std::integral_constant<int, 128>{});
     return hipGetLastError();
 }
 

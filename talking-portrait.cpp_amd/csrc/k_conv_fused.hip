@@ -204,16 +204,19 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
 }
 
 // ---------------------------------------------------------------------------
-// The 64- and 128-channel stages (IC = OC = C): 4 x 32 blocks (the tail's 128
+// The 64-channel stage (IC = OC = 64): 4 x 32 blocks (the tail's 128
 // pixels), four waves.  The halo goes to LDS through registers as above.  The
-// C/32 row blocks of 32 weight rows are split over the waves: C = 64, wave w
-// computes row block w&1 for block rows 2*(w>>1) .. +1; C = 128, row block w
-// for all four block rows.  Every wave reads its A fragments (C/16 of 1 KB
-// per tap) straight from L2 into registers, two taps ahead of the MFMAs: no
-// LDS for A and no barrier inside the conv, so the taps do not wait on one
-// another's memory round trips.  LDS: the halo, then the activated tile
-// (40 KB at C = 64: four workgroups per CU; 73 KB at C = 128: two).  FRAG: A
-// in fragment order (A_ORDER_FRAG), each fragment one contiguous 1 KB.
+// two row blocks of 32 weight rows are split over the waves: wave w computes
+// row block w&1 for block rows 2*(w>>1) .. +1.  Every wave reads its A
+// fragments (C/16 of 1 KB per tap) straight from L2 into registers, two taps
+// ahead of the MFMAs: no LDS for A and no barrier inside the conv, so the taps
+// do not wait on one another's memory round trips.  LDS: the halo, then the
+// activated tile (40 KB: four workgroups per CU).  FRAG: A in fragment order
+// (A_ORDER_FRAG), each fragment one contiguous 1 KB.  The 128- and
+// 256-channel stages run on modconv3x3_hfrag_tail_kernel (k_conv_async.hip:
+// eight waves of 64 rows x 64 pixels, A per 32-channel k tile), which at
+// C = 128 keeps four waves per SIMD against two for this form (r128 at 16
+// frames: 115 -> 108 us).
 template <int C_>
 struct fusedh_cfg {
     static constexpr int C = C_, NT = 256, TH = 4, TW = 32, BN = TH * TW;
@@ -342,15 +345,12 @@ __global__ __launch_bounds__(256) void convh_tail_kernel(ConvParams p, TailArgs 
     tile_tail<TF, TT, C, BN, NT, TW>(ta, so, prm, wfs, n0, tid, sk);
 }
 
-bool modconv_fused64_ok(bool f16, int IC, int OC, int r) {
-    return f16 && IC == OC && (OC == 64 || OC == 128) && r % 32 == 0;
-}
+bool modconv_fused64_ok(bool f16, int IC, int OC, int r) { return f16 && IC == 64 && OC == 64 && r % 32 == 0; }
 
 hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool trunk_f16, bool frag,
                                   hipStream_t st) {
     constexpr int TH = fusedh_cfg<64>::TH;
-    if (p.IC != p.OC || (p.OC != 64 && p.OC != 128) || p.M != p.OC || p.W % 32 != 0 || p.H % TH != 0)
-        return hipErrorInvalidValue;
+    if (p.IC != 64 || p.OC != 64 || p.M != 64 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
@@ -368,8 +368,7 @@ hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool 
         }
 #undef TPMD_L
     };
-    if (p.OC == 64) go(std::integral_constant<int, 64>{});
-    else go(std::integral_constant<int, 128>{});
+    go(std::integral_constant<int, 64>{});
     return hipGetLastError();
 }
 
