@@ -41,16 +41,22 @@ __global__ __launch_bounds__(256) void enc_stem_kernel(const float *__restrict__
     }
 }
 
+// one thread per output pixel and 4 consecutive channels (C % 4 == 0): one
+// 16-byte load per tap and 32-bit index arithmetic; each channel's taps are
+// summed in (row, column) order, out-of-map taps skipped
 template <typename TO>
 __global__ __launch_bounds__(256) void enc_blur_kernel(const float *__restrict__ x, const float *__restrict__ k,
                                                        int H, int W, int C, int pad, int OH, int OW,
                                                        TO *__restrict__ y) {
-    const int64_t total = (int64_t) OH * OW * C;
-    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
-        const int64_t p = i / C;
-        const int c = (int) (i - p * C);
-        const int oy = (int) (p / OW), ox = (int) (p - (int64_t) oy * OW);
-        float acc = 0.0f;
+    const unsigned C4 = (unsigned) C >> 2;
+    const unsigned total = (unsigned) OH * (unsigned) OW * C4;
+    float kk[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) kk[t] = k[t];
+    for (unsigned i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+        const unsigned pix = i / C4, c = (i - pix * C4) * 4u;
+        const int oy = (int) (pix / (unsigned) OW), ox = (int) (pix - (unsigned) oy * (unsigned) OW);
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const int iy = oy + a - pad;
@@ -59,10 +65,17 @@ __global__ __launch_bounds__(256) void enc_blur_kernel(const float *__restrict__
             for (int bb = 0; bb < 4; bb++) {
                 const int ix = ox + bb - pad;
                 if ((unsigned) ix >= (unsigned) W) continue;
-                acc = __builtin_fmaf(k[a * 4 + bb], x[((int64_t) iy * W + ix) * C + c], acc);
+                const floatx4 v = *(const floatx4 *) (x + ((unsigned) (iy * W + ix) * (unsigned) C + c));
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[j] = __builtin_fmaf(kk[a * 4 + bb], v[j], acc[j]);
             }
         }
-        y[i] = enc_cast<TO>(acc);
+        TO *o = y + (size_t) pix * (size_t) C + c;
+        if constexpr (sizeof(TO) == 4) {
+            *(floatx4 *) o = acc;
+        } else {
+            store4<TO>(o, acc[0], acc[1], acc[2], acc[3]);
+        }
     }
 }
 
@@ -250,8 +263,8 @@ hipError_t launch_enc_stem(const float *img, const float *w, const float *b, int
 hipError_t launch_enc_blur(const float *x, const float *k, int H, int W, int C, int pad, void *y, bool y_f16,
                            hipStream_t st) {
     const int OH = H + 2 * pad - 3, OW = W + 2 * pad - 3;
-    if (OH < 1 || OW < 1) return hipErrorInvalidValue;
-    const unsigned g = grid_1d((int64_t) OH * OW * C);
+    if (OH < 1 || OW < 1 || C % 4 != 0 || (int64_t) H * W * C >= (int64_t) 1 << 31) return hipErrorInvalidValue;
+    const unsigned g = grid_1d((int64_t) OH * OW * (C / 4));
     if (y_f16)
         hipLaunchKernelGGL(enc_blur_kernel<half_t>, dim3(g), dim3(256), 0, st, x, k, H, W, C, pad, OH, OW,
                            (half_t *) y);

@@ -97,6 +97,7 @@ struct tpme_ctx {
     float *x1 = nullptr, *sk = nullptr;
     void *xb = nullptr, *sb = nullptr;
     float *app = nullptr, *fch[5] = {}, *motion = nullptr;
+    float *ws = nullptr;         // split-K partials of the deep levels' convs
 
     bool hip_ok(hipError_t e, const char *what) {
         if (e == hipSuccess) return true;
@@ -313,6 +314,16 @@ static int tpme_set_weight_body(tpme_ctx *c, const char *name, const float *data
     return 0;
 }
 
+// split-K factor of an encoder conv: the deep levels' convs have few 64 x 64
+// output tiles (8 at 8 x 8 with 512 channels) against a long k loop (up to
+// 9 * 512 / 32 = 144 k tiles), so their k range is split to give about 256
+// workgroups; the partials are summed in split order by a second pass
+static int enc_splits(int OH, int OW, int OC, int KH, int KW, int IC) {
+    const int tiles = ((OH * OW + 63) / 64) * ((OC + 63) / 64);
+    const int T = KH * KW * IC / 32;
+    return std::max(1, std::min(256 / std::max(tiles, 1), T / 4));
+}
+
 static int tpme_prepare_body(tpme_ctx *c) {
     if (!check(c)) return -1;
     c->free_all();
@@ -357,7 +368,7 @@ static int tpme_prepare_body(tpme_ctx *c) {
     const int R = c->res;
     c->img = (float *) c->dalloc((size_t) 3 * R * R * 4);
     if (!c->img) return -1;
-    size_t x1b = 0, xbb = 0, sbb = 0, skb = 0, xab = 0;
+    size_t x1b = 0, xbb = 0, sbb = 0, skb = 0, xab = 0, wsb = 0;
     for (int l = 0; l <= c->nb; l++) {
         const size_t r = (size_t) c->level_res(l);
         c->lvl[l] = (float *) c->dalloc(r * r * c->level_ch(l) * 4);
@@ -369,8 +380,14 @@ static int tpme_prepare_body(tpme_ctx *c) {
             sbb = std::max(sbb, (r - 1) * (r - 1) * C * 4);
             skb = std::max(skb, (r / 2) * (r / 2) * (size_t) c->cout[l] * 4);
             xab = std::max(xab, r * r * C * 4);
+            const int ri = (int) r, Ci = (int) C, Co = c->cout[l];
+            wsb = std::max(wsb, (size_t) enc_splits(ri, ri, Ci, 3, 3, Ci) * r * r * C * 4);
+            wsb = std::max(wsb, (size_t) enc_splits(ri / 2, ri / 2, Co, 1, 1, Ci) * (r / 2) * (r / 2) * Co * 4);
+            wsb = std::max(wsb, (size_t) enc_splits(ri / 2, ri / 2, Co, 3, 3, Ci) * (r / 2) * (r / 2) * Co * 4);
         }
     }
+    c->ws = (float *) c->dalloc(wsb < 256 ? 256 : wsb);
+    if (!c->ws) return -1;
     c->x1 = (float *) c->dalloc(x1b);
     c->xb = c->dalloc(xbb);
     c->sb = c->dalloc(sbb);
@@ -426,6 +443,8 @@ static int tpme_run_body(tpme_ctx *c, const float *image, int on_device) {
         p.stride = 1;
         p.pad = 1;
         p.OH = p.OW = r;
+        p.ksplit = enc_splits(r, r, C, 3, 3, C);
+        p.ws = c->ws;
         if (!c->hip_ok(launch_enc_conv(p, B.c1.f16, st), "conv1")) return -1;
         // skip: conv1x1 stride 2 of blur(x, pad 1)
         if (!c->hip_ok(launch_enc_blur(c->lvl[i - 1], B.ks, r, r, C, 1, c->sb, B.sk.f16, st), "skip blur")) return -1;
@@ -440,6 +459,8 @@ static int tpme_run_body(tpme_ctx *c, const float *image, int on_device) {
         p.stride = 2;
         p.pad = 0;
         p.OH = p.OW = r / 2;
+        p.ksplit = enc_splits(r / 2, r / 2, Co, 1, 1, C);
+        p.ws = c->ws;
         if (!c->hip_ok(launch_enc_conv(p, B.sk.f16, st), "skip")) return -1;
         // x = leaky(conv3x3 stride 2 of blur(x1, pad 2) + b2) + skip
         if (!c->hip_ok(launch_enc_blur(c->x1, B.k2, r, r, C, 2, c->xb, B.c2.f16, st), "blur")) return -1;
@@ -460,6 +481,8 @@ static int tpme_run_body(tpme_ctx *c, const float *image, int on_device) {
         p.stride = 2;
         p.pad = 0;
         p.OH = p.OW = r / 2;
+        p.ksplit = enc_splits(r / 2, r / 2, Co, 3, 3, C);
+        p.ws = c->ws;
         if (!c->hip_ok(launch_enc_conv(p, B.c2.f16, st), "conv2")) return -1;
     }
     // appearance = the final 4x4 conv on the 4x4 map (one output pixel)
