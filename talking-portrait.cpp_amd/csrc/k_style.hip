@@ -17,7 +17,7 @@ __device__ __forceinline__ int find_seg(const SegTable &t, int row) {
 }
 
 // Both are skinny GEMMs, Y[f][row] = sum_k W[row][k] X[f][k] over 16 frames,
-// run on v_mfma_f32_16x16x4_f32: one wave owns 16 rows x 16 frames.  Lane l
+// run on v_mfma_f32_16x16x4_f32: a wave computes 16 rows x 16 frames.  Lane l
 // feeds A = W[row0 + l%16][k] and B = X[f0 + l%16][k] for k = kb + 4(l/16) + j,
 // j = 0..3 (one MFMA each: a 16-byte load per operand covers four k steps,
 // the k order inside a 16-wide block permuted the same way for both); the
@@ -31,26 +31,47 @@ __device__ __forceinline__ floatx4 mfma16x4_block(const floatx4 a, const floatx4
     return acc;
 }
 
+// Both run one 16-row tile per workgroup with the k range split over its
+// four waves (quarters of the 16-wide k blocks, in order): a wave streams a
+// quarter of the tile's row of W, so the tile's loads are in flight together
+// instead of one wave walking all of K; the four partial tiles are added in
+// wave order through LDS (the same sums for every batch).
+__device__ __forceinline__ floatx4 ksplit_sum(floatx4 acc, int wid, int lane) {
+    __shared__ floatx4 part[3][64];
+    if (wid > 0) part[wid - 1][lane] = acc;
+    __syncthreads();
+    if (wid == 0) {
+#pragma unroll
+        for (int w = 0; w < 3; w++) {
+            const floatx4 b = part[w][lane];
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[j] = acc[j] + b[j];
+        }
+    }
+    return acc;
+}
+
 // style: W = Wmod (all convs' rows, K = 512), X = the latents
 __global__ __launch_bounds__(256) void style_gemv_kernel(const float *__restrict__ Wm,
                                                          const float *__restrict__ bm,
                                                          const float *__restrict__ lat,
                                                          float *__restrict__ s, SegTable seg,
                                                          int nframes) {
-    const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
-    if (r0 >= seg.row0[seg.n]) return;  // whole wave exits together
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * 16;
     const int sg = find_seg(seg, r0);
     const int li = lane & 15, kq = lane >> 4;
     const int f0 = blockIdx.y * 16;
     const int f = f0 + li < nframes ? f0 + li : nframes - 1;
-    const float *wp = Wm + (int64_t) (r0 + li) * 512 + kq * 4;
-    const float *xp = lat + (int64_t) f * 512 + kq * 4;
+    const int k0 = wid * 128;
+    const float *wp = Wm + (int64_t) (r0 + li) * 512 + k0 + kq * 4;
+    const float *xp = lat + (int64_t) f * 512 + k0 + kq * 4;
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (int kb = 0; kb < 512; kb += 16)
+#pragma unroll
+    for (int kb = 0; kb < 128; kb += 16)
         acc = mfma16x4_block(*(const floatx4 *) (wp + kb), *(const floatx4 *) (xp + kb), acc);
-    if (f0 + li < nframes) {
+    acc = ksplit_sum(acc, wid, lane);
+    if (wid == 0 && f0 + li < nframes) {
         const int width = seg.width[sg];
         float *out = s + seg.out0[sg] + (int64_t) (f0 + li) * width + (r0 - seg.row0[sg]) + kq * 4;
 #pragma unroll
@@ -65,9 +86,8 @@ __global__ __launch_bounds__(256) void demod_kernel(const float *__restrict__ sa
                                                     float *__restrict__ inv_den, DemodTable t,
                                                     int nframes) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
-    if (r0 >= t.row0[t.n]) return;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * 16;
     int c = 0;
     while (c + 1 < t.n && r0 >= t.row0[c + 1]) c++;
     const int o0 = r0 - t.row0[c];
@@ -76,18 +96,21 @@ __global__ __launch_bounds__(256) void demod_kernel(const float *__restrict__ sa
     const int li = lane & 15, kq = lane >> 4;
     const int f0 = blockIdx.y * 16;
     const int f = f0 + li < nframes ? f0 + li : nframes - 1;
+    // this wave's quarter of the IC / 16 k blocks
+    const int nb = IC / 16, kb0 = (wid * nb) / 4 * 16, kb1 = ((wid + 1) * nb) / 4 * 16;
     const float *wp = S + (int64_t) (o0 + li) * IC + kq * 4;
     const float *xp = s + t.s0[c] + (int64_t) f * IC + kq * 4;
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
-    for (int kb = 0; kb < IC; kb += 16) {
+    for (int kb = kb0; kb < kb1; kb += 16) {
         const floatx4 x = *(const floatx4 *) (xp + kb);
         floatx4 x2;
 #pragma unroll
         for (int j = 0; j < 4; j++) x2[j] = x[j] * x[j];
         acc = mfma16x4_block(*(const floatx4 *) (wp + kb), x2, acc);
     }
-    if (f0 + li < nframes) {
+    acc = ksplit_sum(acc, wid, lane);
+    if (wid == 0 && f0 + li < nframes) {
         float *out = inv_den + t.d0[c] + (int64_t) (f0 + li) * OC + o0 + kq * 4;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
@@ -136,8 +159,8 @@ hipError_t launch_style_gemv(const float *Wm, const float *bm, const float *lat,
     for (int i = 0; i <= seg.n; i++)
         if (seg.row0[i] % 16 != 0) return hipErrorInvalidValue;
     const int tiles = R / 16;
-    hipLaunchKernelGGL(style_gemv_kernel, dim3((tiles + 3) / 4, (nframes + 15) / 16), dim3(256), 0, st, Wm, bm,
-                       lat, s, seg, nframes);
+    hipLaunchKernelGGL(style_gemv_kernel, dim3(tiles, (nframes + 15) / 16), dim3(256), 0, st, Wm, bm, lat, s, seg,
+                       nframes);
     return hipGetLastError();
 }
 
@@ -150,8 +173,8 @@ hipError_t launch_demod(const float *saug, const float *s, float *inv_den, const
             t.s0[i] % 4 != 0)
             return hipErrorInvalidValue;
     const int tiles = R / 16;
-    hipLaunchKernelGGL(demod_kernel, dim3((tiles + 3) / 4, (nframes + 15) / 16), dim3(256), 0, st, saug, s,
-                       inv_den, t, nframes);
+    hipLaunchKernelGGL(demod_kernel, dim3(tiles, (nframes + 15) / 16), dim3(256), 0, st, saug, s, inv_den, t,
+                       nframes);
     return hipGetLastError();
 }
 
