@@ -7,7 +7,7 @@
 
 namespace tpmd {
 
-template <typename TF, typename TOUT, typename TT, int G>
+template <typename TF, typename TOUT, typename TT, int G, bool FGR>
 __global__ __launch_bounds__(256) void stage_tail_kernel(TailArgs a) {
     constexpr int PPW = 64 / G;  // pixels per wave
     const int lane = threadIdx.x & 63;
@@ -16,14 +16,14 @@ __global__ __launch_bounds__(256) void stage_tail_kernel(TailArgs a) {
     const int64_t wave = (int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int64_t nwaves = (int64_t) gridDim.x * (blockDim.x >> 6);
     TailWeights w;
-    load_tail_weights(a, gl * 8, w);
+    load_tail_weights<FGR>(a, gl * 8, w);
     for (int64_t base = wave * PPW; base < P; base += nwaves * PPW) {
         const int64_t p = base + grp;
         const bool valid = p < P;
         const int64_t pp = valid ? p : P - 1;
         float ov[8];
         load8<TOUT>::run((const TOUT *) a.out + pp * a.C + gl * 8, ov);
-        tail_pixel<TF, TT, G>(a, pp, valid, gl, ov, w);
+        tail_pixel<TF, TT, G, FGR>(a, pp, valid, gl, ov, w);
     }
 }
 
@@ -35,10 +35,14 @@ static hipError_t launch_tail_typed(const TailArgs &a, hipStream_t st) {
     int64_t nb = (P + ppb - 1) / ppb;
     if (nb > 65536) nb = 65536;
     if (nb < 1) nb = 1;
-#define TPMD_T(g)                                                                                \
-    case g:                                                                                      \
-        hipLaunchKernelGGL((stage_tail_kernel<TF, TOUT, TT, g>), dim3((unsigned) nb), dim3(256), 0, \
-                           st, a);                                                               \
+#define TPMD_T(g)                                                                                       \
+    case g:                                                                                             \
+        if (a.featg)                                                                                    \
+            hipLaunchKernelGGL((stage_tail_kernel<TF, TOUT, TT, g, true>), dim3((unsigned) nb), dim3(256), 0, \
+                               st, a);                                                                  \
+        else                                                                                            \
+            hipLaunchKernelGGL((stage_tail_kernel<TF, TOUT, TT, g, false>), dim3((unsigned) nb), dim3(256), 0, \
+                               st, a);                                                                  \
         break;
     switch (G) {
         TPMD_T(4) TPMD_T(8) TPMD_T(16) TPMD_T(32) TPMD_T(64)

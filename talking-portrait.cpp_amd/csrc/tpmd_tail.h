@@ -57,115 +57,13 @@ struct TailWeights {
     float wf[3][8], wr[3][8];
 };
 
+// (FGR: the ToRGB sum comes from TailArgs::featg, the ToRGB slice is not needed)
+template <bool FGR>
 __device__ __forceinline__ void load_tail_weights(const TailArgs &a, int c0, TailWeights &w) {
 #pragma unroll
     for (int k = 0; k < 3; k++) {
         load8<float>::run(a.wflow + k * a.C + c0, w.wf[k]);
-        load8<float>::run(a.wrgb + k * a.C + c0, w.wr[k]);
-    }
-}
-
-// One pixel pp = frame * r*r + y*r + x of the batch; `valid` false for the
-// padding lanes of the last group (they take part in the butterflies and
-// store nothing).  ov: this lane's 8 dense-conv output channels (f32).
-template <typename TF, typename TT, int G>
-__device__ __forceinline__ void tail_pixel(const TailArgs &a, int64_t pp, bool valid, int gl,
-                                           const float ov[8], const TailWeights &w) {
-    // one rounding per operation everywhere; the two dot products use explicit fma
-#pragma clang fp contract(off)
-    const int c0 = gl * 8;
-    const int r = a.r, C = a.C, rh = r >> 1;
-    const int64_t RR = (int64_t) r * r;
-    const int fr = (int) (pp / RR);
-    const int pix = (int) (pp - (int64_t) fr * RR);
-    const int y = pix / r, x = pix - y * r;
-
-    // ---- ToFlow: (Wf * s_f) . out, folded weight rounded like gemm_weight
-    float sf[8];
-    load8<float>::run(a.sflow + (int64_t) fr * C + c0, sf);
-    float fl[3];
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float wv = w.wf[k][e] * sf[e];
-            acc = __builtin_fmaf(wv, ov[e], acc);
-        }
-        fl[k] = group_sum<G>(acc);
-    }
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        fl[k] = fl[k] + a.fbias[k];
-        if (a.flow_prev)
-            fl[k] = fl[k] + upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
-    }
-    if (a.flow_cur && valid && gl < 3) {
-        const float v = gl == 0 ? fl[0] : (gl == 1 ? fl[1] : fl[2]);
-        a.flow_cur[((int64_t) fr * 3 + gl) * RR + pix] = v;
-    }
-
-    // ---- flow head + gather
-    const float gx = tanhf(fl[0]) + a.lin[x];
-    const float gy = tanhf(fl[1]) + a.lin[y];
-    const float m = 1.0f / (1.0f + expf(-fl[2]));
-    const taps4 t = gather_geometry(gx, gy, r, r);
-    float fv[4][8];
-    bool in[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {  // issue the four tap loads together
-        in[k] = tap_inside(t, k, r, r);
-        if (in[k])
-            load8<TF>::run((const TF *) a.feat + (int64_t) ((t.y0 + (k >> 1)) * r + t.x0 + (k & 1)) * C + c0,
-                           fv[k]);
-    }
-    float smp[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) smp[e] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        if (!in[k]) continue;
-        const float wk = tap_weight(t, k);
-#pragma unroll
-        for (int e = 0; e < 8; e++) smp[e] += wk * fv[k][e];
-    }
-
-    // ---- warp / trunk
-    float warp[8], trunk[8];
-    const float one_m = 1.0f - m;
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        warp[e] = smp[e] * m;
-        trunk[e] = warp[e] + ov[e] * one_m;
-    }
-    if (valid && a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
-    if (valid && a.trunk) {
-        if (a.s_next) {
-            float sn[8];
-            load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
-#pragma unroll
-            for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
-        }
-        store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
-    }
-
-    // ---- ToRGB
-    float rgb[3];
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc = __builtin_fmaf(w.wr[k][e], warp[e], acc);
-        rgb[k] = group_sum<G>(acc);
-    }
-    if (valid && gl < 3) {
-        const int k = gl;
-        const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
-        float v = leaky(rv + a.rlb[k]);
-        v = v + a.rbias[k];
-        if (a.rgb_prev)
-            v = v + upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
-        a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
+        if constexpr (!FGR) load8<float>::run(a.wrgb + k * a.C + c0, w.wr[k]);
     }
 }
 
@@ -556,6 +454,124 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     if (TAIL_FEATG_OVERLAP && tid < BN) {
         const float skr[3] = {sk.rgb[0], sk.rgb[1], sk.rgb[2]};
         tail_featg_finish(a, gt, gm, fr, tile_pix<TWC>(pix0, r, tid), skr, gv);
+    }
+}
+
+// One pixel pp = frame * r*r + y*r + x of the batch; `valid` false for the
+// padding lanes of the last group (they take part in the butterflies and
+// store nothing).  ov: this lane's 8 dense-conv output channels (f32).
+template <typename TF, typename TT, int G, bool FGR>
+__device__ __forceinline__ void tail_pixel(const TailArgs &a, int64_t pp, bool valid, int gl,
+                                           const float ov[8], const TailWeights &w) {
+    // one rounding per operation everywhere; the two dot products use explicit fma
+#pragma clang fp contract(off)
+    const int c0 = gl * 8;
+    const int r = a.r, C = a.C, rh = r >> 1;
+    const int64_t RR = (int64_t) r * r;
+    const int fr = (int) (pp / RR);
+    const int pix = (int) (pp - (int64_t) fr * RR);
+    const int y = pix / r, x = pix - y * r;
+
+    // ---- ToFlow: (Wf * s_f) . out, folded weight rounded like gemm_weight
+    float sf[8];
+    load8<float>::run(a.sflow + (int64_t) fr * C + c0, sf);
+    float fl[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float wv = w.wf[k][e] * sf[e];
+            acc = __builtin_fmaf(wv, ov[e], acc);
+        }
+        fl[k] = group_sum<G>(acc);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        fl[k] = fl[k] + a.fbias[k];
+        if (a.flow_prev)
+            fl[k] = fl[k] + upfirdn2x_at(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y);
+    }
+    if (a.flow_cur && valid && gl < 3) {
+        const float v = gl == 0 ? fl[0] : (gl == 1 ? fl[1] : fl[2]);
+        a.flow_cur[((int64_t) fr * 3 + gl) * RR + pix] = v;
+    }
+
+    // ---- flow head + gather
+    const float gx = tanhf(fl[0]) + a.lin[x];
+    const float gy = tanhf(fl[1]) + a.lin[y];
+    const float m = 1.0f / (1.0f + expf(-fl[2]));
+    const taps4 t = gather_geometry(gx, gy, r, r);
+    float fv[4][8];
+    bool in[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {  // issue the four tap loads together
+        in[k] = tap_inside(t, k, r, r);
+        if (in[k])
+            load8<TF>::run((const TF *) a.feat + (int64_t) ((t.y0 + (k >> 1)) * r + t.x0 + (k & 1)) * C + c0,
+                           fv[k]);
+    }
+    float smp[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) smp[e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if (!in[k]) continue;
+        const float wk = tap_weight(t, k);
+#pragma unroll
+        for (int e = 0; e < 8; e++) smp[e] += wk * fv[k][e];
+    }
+
+    // ---- warp / trunk
+    float warp[8], trunk[8];
+    const float one_m = 1.0f - m;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        warp[e] = smp[e] * m;
+        trunk[e] = warp[e] + ov[e] * one_m;
+    }
+    if (valid && a.warp_tap) store8<float>(a.warp_tap + pp * C + c0, warp);
+    if (valid && a.trunk) {
+        if (a.s_next) {
+            float sn[8];
+            load8<float>::run(a.s_next + (int64_t) fr * C + c0, sn);
+#pragma unroll
+            for (int e = 0; e < 8; e++) trunk[e] = trunk[e] * sn[e];
+        }
+        store8<TT>((TT *) a.trunk + pp * C + c0, trunk);
+    }
+
+    // ---- ToRGB: from the per-feature-pixel Wr . feat (FGR, TailArgs::featg
+    // set: lane 0 stores the pixel's three values), else a dot over the G
+    // lanes' channels
+    if constexpr (FGR) {
+        if (valid && gl == 0) {
+            tail_skip sk{};
+            if (a.rgb_prev) {
+#pragma unroll
+                for (int k = 0; k < 3; k++)
+                    sk.rgb[k] = upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+            }
+            tail_featg_rgb(a, t, m, fr, pix, sk);
+        }
+        return;
+    }
+    float rgb[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc = __builtin_fmaf(w.wr[k][e], warp[e], acc);
+        rgb[k] = group_sum<G>(acc);
+    }
+    if (valid && gl < 3) {
+        const int k = gl;
+        const float rv = k == 0 ? rgb[0] : (k == 1 ? rgb[1] : rgb[2]);
+        float v = leaky(rv + a.rlb[k]);
+        v = v + a.rbias[k];
+        if (a.rgb_prev)
+            v = v + upfirdn2x_at(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y);
+        a.rgb_cur[((int64_t) fr * 3 + k) * RR + pix] = v;
     }
 }
 
