@@ -502,14 +502,12 @@ __device__ __forceinline__ void tail_pixel(const TailArgs &a, int64_t pp, bool v
     const float gy = tanhf(fl[1]) + a.lin[y];
     const float m = 1.0f / (1.0f + expf(-fl[2]));
     const taps4 t = gather_geometry(gx, gy, r, r);
-    float fv[4][8];
+    feat8<TF> fv[4];  // kept in the stored type until used
     bool in[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {  // issue the four tap loads together
         in[k] = tap_inside(t, k, r, r);
-        if (in[k])
-            load8<TF>::run((const TF *) a.feat + (int64_t) ((t.y0 + (k >> 1)) * r + t.x0 + (k & 1)) * C + c0,
-                           fv[k]);
+        if (in[k]) fv[k].load((const TF *) a.feat + (int64_t) ((t.y0 + (k >> 1)) * r + t.x0 + (k & 1)) * C + c0);
     }
     float smp[8];
 #pragma unroll
