@@ -404,6 +404,20 @@ def main():
     r["traffic"] = measured_traffic(r["kernel"])
     r.pop("us")
 
+    # the f16 MFMA rate this GPU sustains (its clock drops under a matrix
+    # load by an amount set by the operand bits): the dominant kernel's
+    # fraction of it, beside the fraction of the published peak
+    sustained = None
+    if args.ftype == "f16":
+        tf_rand, ghz_rand = tpmd.probe_mfma_f16(True)
+        tf_zero, ghz_zero = tpmd.probe_mfma_f16(False)
+        sustained = {"random_operands_tflops": round(tf_rand, 1), "random_operands_core_ghz": round(ghz_rand, 2),
+                     "zero_operands_tflops": round(tf_zero, 1), "zero_operands_core_ghz": round(ghz_zero, 2),
+                     "note": "back-to-back v_mfma_f32_32x32x16_f16, four waves per SIMD, no memory traffic "
+                             "(tpmd_probe_mfma_f16)"}
+        if r["bound"] == "mfma":
+            r["frac_of_sustained"] = round(r["achieved"] / tf_rand, 4)
+
     out = {
         "metric": "motion-decoder frames/sec @512x512 f16, 1 GPU",
         "value": round(fps, 2),
@@ -427,6 +441,8 @@ def main():
         "lanes": args.lanes,
         "graphs": not args.no_graphs,
     }
+    if sustained:
+        out["mfma_sustained"] = sustained
     if args.decoder_only:
         if args.copy_probe:
             copy_probe()

@@ -241,6 +241,17 @@ int tpmd_set_graphs(tpmd_ctx *ctx, int enable);
 int tpmd_profile_stages(tpmd_ctx *ctx, int enable);
 int tpmd_stage_times(const tpmd_ctx *ctx, float *us, int max_slots);
 
+/* Sustained f16 MFMA rate of this GPU (no counterpart in the reference: the
+ * benchmark's roofline reads it beside the published peak).  Every SIMD
+ * runs four waves of independent v_mfma_f32_32x32x16_f16 on all-zero
+ * (random_operands = 0) or pseudo-random f16 operands in [-1, 1) for `iters`
+ * iterations of 8 MFMAs; *tflops gets the rate over 10 timed launches and
+ * *core_ghz the core clock one wave saw.  The MI355X lowers its clock under
+ * such a load by an amount that depends on the operand bits, so the random
+ * figure is the ceiling of an MFMA-bound kernel.  Synchronous on the null
+ * stream; allocates and frees a small device buffer.  Returns 0 or -1. */
+int tpmd_probe_mfma_f16(int random_operands, int iters, float *tflops, float *core_ghz);
+
 /* ---- per-stage entry points on DEVICE buffers (f32 in / f32 out) -------
  * These run one piece of the decoder with the context's weights, for
  * parity tests and per-stage measurement.  `stream` is a hipStream_t

@@ -75,6 +75,7 @@ def lib():
             "tpmd_set_graphs": (I, [P, I]),
             "tpmd_profile_stages": (I, [P, I]),
             "tpmd_stage_times": (I, [P, P, I]),
+            "tpmd_probe_mfma_f16": (I, [I, I, P, P]),
             "tpmd_set_tap": (I, [P, I, I, P, I64]),
             "tpmd_decode_taps": (I, [P, P, P, P, P]),
             "tpmd_tap_frame_bytes": (I64, [P, I, I]),
@@ -444,6 +445,16 @@ def flow_grid(fl, xs, stream=None):
     if rc != 0:
         raise TpmdError("tpmd_flow_grid: invalid arguments")
     return y
+
+
+def probe_mfma_f16(random_operands=True, iters=2000):
+    """(TFLOP/s, core GHz) of back-to-back f16 MFMAs on every SIMD with zero
+    or random operands (tpmd_probe_mfma_f16)"""
+    tf, ghz = ctypes.c_float(), ctypes.c_float()
+    rc = lib().tpmd_probe_mfma_f16(1 if random_operands else 0, iters, ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise TpmdError("tpmd_probe_mfma_f16 failed")
+    return float(tf.value), float(ghz.value)
 
 
 class MotionEncoder:

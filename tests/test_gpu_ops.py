@@ -101,3 +101,14 @@ def test_flow_grid(om, torch_cuda):
     want = om.flow_grid(fl, xs)
     got = tpmd.flow_grid(_dev(torch, fl), _dev(torch, xs)).cpu().numpy()
     assert np.abs(got - want).max() < 4e-7
+
+
+def test_mfma_probe(torch_cuda):
+    # the sustained-rate probe the benchmark reports: a rate between 5 % and
+    # 100 % of the 2.5 PFLOP/s f16 peak and a core clock of a plausible
+    # gfx950 value for each operand kind; bad arguments are refused
+    for random_operands in (True, False):
+        tf, ghz = tpmd.probe_mfma_f16(random_operands, iters=200)
+        assert 125.0 < tf <= 2600.0
+        assert 0.3 < ghz < 3.0
+    assert tpmd.lib().tpmd_probe_mfma_f16(1, 0, None, None) == -1
