@@ -27,6 +27,8 @@ def _dev(torch, a):
     (2048, 6, 5, 123, -1.2, 1.2, False, True, False),
     (4, 33, 17, 5000, -1.1, 1.1, False, False, False),      # one lane per point
     (8, 17, 33, 5000, -1.1, 1.1, True, False, False),
+    (1024, 64, 64, 5000, -1.2, 1.2, True, False, False),    # 8 MB map: channel slices over the XCDs
+    (512, 70, 60, 3000, -1.3, 1.3, False, True, False),     # sliced, map edges off the 32-pixel grid
 ])
 def test_gather_bit_exact(om, torch_cuda, C, W, H, N, lo, hi, f16, planar, sp):
     torch = torch_cuda
