@@ -27,7 +27,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-munsafe-fp-atomics"]
 
-SOURCES = ["k_gather.hip", "k_conv.hip", "k_conv_async.hip", "k_conv_fused.hip", "k_conv_up.hip", "k_conv_halo.hip", "k_tail.hip", "k_style.hip", "k_enc.hip", "k_fmt.hip", "k_probe.hip", "tpmd.cpp", "tpme.cpp", "tpfm.cpp"]
+SOURCES = ["k_gather.hip", "k_conv.hip", "k_conv_async.hip", "k_conv_hfrag.hip", "k_conv_hfrag8.hip", "k_conv_hfrag16.hip", "k_conv_hfrag_tail.hip", "k_conv_fused.hip", "k_conv_up.hip", "k_conv_halo.hip", "k_tail.hip", "k_style.hip", "k_enc.hip", "k_fmt.hip", "k_probe.hip", "tpmd.cpp", "tpme.cpp", "tpfm.cpp"]
 # plain C++ over the C ABI (no HIP): the tp::motion_dec shim, in the library
 HOST_SOURCES = ["motion_dec.cpp", "motion_enc.cpp", "gguf.cpp", "gguf_abi.cpp"]
 CXX = os.environ.get("CXX", "g++")

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
 // do not wait on one another's memory round trips.  LDS: the halo, then the
 // activated tile (40 KB: four workgroups per CU).  FRAG: A in fragment order
 // (A_ORDER_FRAG), each fragment one contiguous 1 KB.  The 128- and
-// 256-channel stages run on modconv3x3_hfrag_tail_kernel (k_conv_async.hip:
+// 256-channel stages run on modconv3x3_hfrag_tail_kernel (k_conv_hfrag_tail.hip:
 // eight waves of 64 rows x 64 pixels, A per 32-channel k tile), which at
 // C = 128 keeps four waves per SIMD against two for this form (r128 at 16
 // frames: 115 -> 108 us).

@@ -120,12 +120,12 @@ hipError_t launch_modconv_async(const ConvParams &p, int mode, int epi, int nspl
 // k_conv_async.hip: f16 dense conv + fused stage tail for OC in {32, 64, 128,
 // 256} (tiles of 256, 128, 128, 128 pixels of one frame) with the same ring
 bool modconv_tail_async_ok(int OC, int r);
-// k_conv_async.hip: f16 dense conv + fused stage tail for IC = OC = 256 on
+// k_conv_hfrag_tail.hip: f16 dense conv + fused stage tail for IC = OC = 128 or 256 on
 // the halo conv (4 x 32 pixel blocks, A in A_ORDER_FRAG)
 bool modconv_hfrag_tail_ok(bool f16, int IC, int OC, int H, int W);
 hipError_t launch_modconv_hfrag_tail(const ConvParams &p, const TailArgs &ta, bool trunk_f16, hipStream_t st);
 // 256- or 128-row tiles over 8 x 32 or 16 x 16 pixel blocks with the input
-// halo in LDS and A read from L2 in fragment order (k_conv_async.hip,
+// halo in LDS and A read from L2 in fragment order (k_conv_hfrag.hip,
 // A_ORDER_FRAG); f16 output, or f32 output of a dense conv
 bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W);
 hipError_t launch_modconv_hfrag(ConvParams p, int mode, bool out_f16, hipStream_t st);
