@@ -6,11 +6,14 @@
 //   * a workgroup owns a TH x 32 block of output pixels of one frame; the
 //     (TH+2) x 34 input pixels around it (zero outside the map) go through
 //     registers to LDS with a 16-byte pad per pixel (conflict-free 32-pixel
-//     fragment reads); the 32 x 288 weight matrix goes global -> LDS by the
-//     DMA path in MFMA fragment order (18 fragments of 1 KB, each read back
-//     by one ds_read_b128 per lane), so it holds no registers.  FRAG: A is
-//     stored in that order (A_ORDER_FRAG), so each fragment's DMA reads
-//     1 KB of contiguous memory instead of 32 bytes of 32 rows;
+//     fragment reads); FRAG (A stored in MFMA fragment order, A_ORDER_FRAG:
+//     18 fragments of 1 KB): every wave reads the 32 x 288 weight matrix
+//     from L2 straight into registers, each tap's two fragments two taps
+//     ahead of its MFMAs, so the LDS holds only the halo (49.5 KB: three
+//     workgroups per CU at six waves per SIMD, 80 registers, against two when
+//     A sat in LDS too; measured at r512, 16 frames: 194.6 -> 184.1 us on
+//     synthetic operands, bit-identical); tap-major A goes global -> LDS by
+//     the DMA path instead (one fragment of 32 rows x 16 bytes per DMA);
 //   * wave w computes rows w*RPW .. of the block (RPW = 2): for each tap (dy, dx) and
 //     16-channel step, the B fragment is the halo row shifted by (dy, dx);
 //   * the activated tile goes to LDS over the halo and the two-phase stage
@@ -40,7 +43,7 @@ namespace tpmd {
 constexpr int F32_NT = 512;
 constexpr bool F32_SWZ = false;
 
-template <int TH, bool FG = false>
+template <int TH, bool FG = false, bool AREG = false>
 struct fused32_cfg {
     static constexpr int C = 32, NT = F32_NT, TW = 32, BN = TH * TW;
     static constexpr int HWD = TW + 2, HPX = (TH + 2) * HWD;
@@ -55,7 +58,7 @@ struct fused32_cfg {
     typedef tile_tail_lds<C, BN> L;
     static constexpr int HALO = HPX * PXB;
     static constexpr int AOFF = (HALO + 255) / 256 * 256;  // A fragments, fragment-major
-    static constexpr int CONV = AOFF + NAF * 1024;          // conv-phase LDS
+    static constexpr int CONV = AOFF + (AREG ? 0 : NAF * 1024);  // conv-phase LDS
     static constexpr int TAIL = FG ? 0 : L::WFS0 * 4;       // so + prm, over the conv's LDS
     static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
     static constexpr int LDS = WFS + 3 * C * 4;
@@ -65,10 +68,11 @@ struct fused32_cfg {
 };
 
 template <typename TF, typename TT, int TH, bool FRAG, bool FG>
-__global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailArgs ta, int tiles_x,
-                                                             int tiles_frame) {
+__global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) void conv32_tail_kernel(
+    ConvParams p, TailArgs ta, int tiles_x, int tiles_frame) {
     typedef half_t TA;
-    typedef fused32_cfg<TH, FG> F;
+    constexpr bool AREG = FRAG;                 // A fragments from L2 into registers
+    typedef fused32_cfg<TH, FG, AREG> F;
     typedef typename F::L L;
     constexpr int C = F::C, NT = F::NT, TW = F::TW, BN = F::BN, HWD = F::HWD, PXB = F::PXB;
     constexpr int CPP = F::CPP, HCH = F::HCH, PF = F::PF, KS = F::KS, NAF = F::NAF, RPW = F::RPW;
@@ -105,11 +109,19 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
         });
     });
     const int lrow = lane & 31, khalf = lane >> 5;
-    {
-        // fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
-        const TA *arow = FRAG ? (const TA *) p.A + lane * 8 : (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
+    // A fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
+    u32x4 areg[3][KS];   // AREG: tap t's fragments in set t % 3, requested two taps ahead
+    const TA *afr = (const TA *) p.A + lane * 8;
+    auto load_a = [&](int tap, u32x4 (&dst)[KS]) {
+        static_for<KS>([&](auto s) { dst[s] = *(const u32x4 *) (afr + (tap * KS + s) * 512); });
+    };
+    if constexpr (AREG) {
+        load_a(0, areg[0]);
+        load_a(1, areg[1]);
+    } else {
+        const TA *arow = (const TA *) p.A + (int64_t) lrow * K + khalf * 8;
         for (int f = wid; f < NAF; f += NT / 64)
-            __builtin_amdgcn_global_load_lds((const void *) (arow + f * (FRAG ? 512 : 16)),
+            __builtin_amdgcn_global_load_lds((const void *) (arow + f * 16),
                                              (__attribute__((address_space(3))) void *) (smem + F::AOFF + f * 1024),
                                              16, 0, 0);
     }
@@ -122,7 +134,7 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
         }
     });
     tile_tail_wfs_store<C, NT>(wfs, tid, wr);
-    __syncthreads();  // (waits for the A fragments' DMA too)
+    __syncthreads();  // (waits for the A fragments' DMA too, when A goes through LDS)
 
     // conv: acc[b] = 32 channels x the 32 pixels of output row wid*RPW + b
     floatx16 acc[RPW];
@@ -132,11 +144,14 @@ __global__ __launch_bounds__(F32_NT) void conv32_tail_kernel(ConvParams p, TailA
     });
     static_for<9>([&](auto tap) {
         constexpr int dy = tap / 3, dx = tap % 3;  // halo offsets of the tap
+        if constexpr (AREG && tap + 2 < 9) load_a(tap + 2, areg[(tap + 2) % 3]);
         static_for<KS>([&](auto ks) {
             static_for<RPW>([&](auto b) {
                 const int hrow = wid * RPW + b + dy;
                 const u32x4 bf = *(const u32x4 *) (smem + F::hoff(hrow * HWD + lrow + dx, ks * 2 + khalf));
-                const u32x4 af = *(const u32x4 *) (smem + F::AOFF + (tap * KS + ks) * 1024 + lane * 16);
+                u32x4 af;
+                if constexpr (AREG) af = areg[tap % 3][ks];
+                else af = *(const u32x4 *) (smem + F::AOFF + (tap * KS + ks) * 1024 + lane * 16);
                 mfma_op<TA>::run(af, bf, acc[b]);
             });
         });
