@@ -40,11 +40,14 @@ int round32(int v) { return (v + 31) / 32 * 32; }
 
 // split-K factor of a linear layer over `rows` tokens: about 1024
 // workgroups (the GEMM's 64 x 64 tiles are few at 180 rows, and a short k
-// loop per workgroup hides the load latency), at least 2 k tiles each
+// loop per workgroup hides the load latency), at least 2 k tiles each, and
+// at most 8 splits, whose f32 partials of all rows are written and read back
+// (measured on MI355X, a 50-frame chunk: no cap 8.2 ms, at most 8 splits
+// 7.6-7.7, at most 4 8.0-8.2, at most 2 10.2-10.3)
 int lin_splits(int rows, int out, int in) {
     const int tiles = ((rows + 63) / 64) * ((out + 63) / 64);
     const int T = in / 32;
-    return std::max(1, std::min(1024 / std::max(tiles, 1), T / 2));
+    return std::max(1, std::min(std::min(1024 / std::max(tiles, 1), T / 2), 8));
 }
 
 }  // namespace

@@ -42,8 +42,11 @@ static __device__ __attribute__((aligned(16))) unsigned int halo_zero16[4];
 //     decoder; the r128 and r256 up-convs measured the same either way);
 //   * 128 rows x 8 x 32 or x 16 x 16 pixels where 256 rows leave fewer than
 //     256 tiles at 16 frames (the r32 convs: a 32 x 32 map, a 16 x 16 up-conv
-//     input): eight waves of 64 x 64, and for the IC = 512 up-conv on 16 x 16
-//     blocks (the r32 up-conv) four waves of 64 x 128 (76 -> 72 us);
+//     input): eight waves of 64 x 64, and for IC = 512 four waves of 64 x 128:
+//     the up-conv on 16 x 16 blocks (the r32 up-conv, 76 -> 72 us) and the
+//     dense conv with f32 output (the r32 dense conv, whose f32 stage then
+//     goes out in two passes of 128 pixels, 67.6 KB, two workgroups per CU:
+//     78 -> 76 us);
 // f16 output, or f32 output of a dense conv on 128 rows.  The output goes
 // through an LDS stage ([pixel][row], f16 or f32) and is written as whole
 // 16-byte chunks of contiguous memory.
@@ -66,7 +69,11 @@ __global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p
     typedef hfrag_cfg<BM, TH, TW, NW_, TM_> F;
     constexpr int NW = F::NW, NT = F::NT, WN = F::WN, BN = F::BN, TM = F::TM, TN = F::TN;
     constexpr int HWD = F::HWD, HPX = F::HPX, LPH = F::LPH;
-    constexpr int ORS = BM * (int) sizeof(TO) + 16, OUT = BN * ORS;  // staged output, one padded row per pixel
+    // staged output, one padded row per pixel; f32 output of four waves goes
+    // through in two passes of half the pixels (each pass the tile of half
+    // the wave columns), so its stage fits beside a second workgroup
+    constexpr int ORS = BM * (int) sizeof(TO) + 16;
+    constexpr int NP = sizeof(TO) == 4 && NW == 4 && WN % 2 == 0 ? 2 : 1, BNP = BN / NP, OUT = BNP * ORS;
     constexpr int LDS = 2 * HR_HBUF > OUT ? 2 * HR_HBUF : OUT;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
 
@@ -182,40 +189,12 @@ __global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p
     });
 
     // store epilogue: the tile is staged in LDS as [pixel][row] (ORS-byte
-    // rows) and written back as whole 16-byte chunks of contiguous output
-    __syncthreads();
-    static_for<TN>([&](auto b) {
-        const int nl = (wn * TN + b) * 32 + lrow;
-        static_for<TM>([&](auto a) {
-            static_for<4>([&](auto i) {
-                const int ml = (wm * TM + a) * 32 + i * 8 + khalf * 4;
-                const int m = m0 + ml;
-                const int o = MODE == MODE_DENSE ? m : m % p.OC;
-                const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + o);
-                const floatx4 bb = *(const floatx4 *) (p.bias + o);
-                floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
-                if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + o);
-                floatx4 v;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
-                    if (p.out_scale) v[j] *= sc[j];
-                }
-                if constexpr (sizeof(TO) == 2) {
-                    half4 hv;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) hv[j] = (half_t) v[j];
-                    *(half4 *) (smem + nl * ORS + ml * 2) = hv;
-                } else {
-                    *(floatx4 *) (smem + nl * ORS + ml * 4) = v;
-                }
-            });
-        });
-    });
-    __syncthreads();
+    // rows) and written back as whole 16-byte chunks of contiguous output,
+    // in NP passes of BNP pixels (pass h: the waves of wave columns
+    // h*WN/NP ..)
     constexpr int EPC = 16 / (int) sizeof(TO);           // output elements per 16-byte chunk
-    constexpr int CPR = BM / EPC, NCH = BN * CPR, STEP = NT / CPR;
-    static_assert(NCH % NT == 0 && NT % CPR == 0, "store pass");
+    constexpr int CPR = BM / EPC, NCH = BNP * CPR, STEP = NT / CPR;
+    static_assert(NCH % NT == 0 && NT % CPR == 0 && WN % NP == 0, "store pass");
     const int mc = tid % CPR;
     const int m = m0 + mc * EPC;
     int cls = 0, o = m;
@@ -225,14 +204,50 @@ __global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p
     }
     const int64_t HW = (int64_t) H * W;
     TO *Yp = (TO *) p.Y;
-    static_for<NCH / NT>([&](auto j) {
-        const int nl = tid / CPR + j * STEP;
-        const int y = y0 + nl / TW, x = x0 + nl % TW;
-        int64_t opix;
-        if constexpr (MODE == MODE_DENSE) opix = fr * HW + (int64_t) y * W + x;
-        else opix = fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
-        const u32x4 v = *(const u32x4 *) (smem + nl * ORS + mc * 16);
-        *(u32x4 *) (Yp + opix * p.OC + o) = v;
+    static_for<NP>([&](auto hh) {
+        constexpr int h = decltype(hh)::value;
+        __syncthreads();   // the halo's (h = 0) or the previous pass's reads are done
+        if (wn / (WN / NP) == h) {
+            static_for<TN>([&](auto b) {
+                const int nl = (wn * TN + b) * 32 + lrow - h * BNP;
+                static_for<TM>([&](auto a) {
+                    static_for<4>([&](auto i) {
+                        const int ml = (wm * TM + a) * 32 + i * 8 + khalf * 4;
+                        const int mr = m0 + ml;
+                        const int orow = MODE == MODE_DENSE ? mr : mr % p.OC;
+                        const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * p.OC + orow);
+                        const floatx4 bb = *(const floatx4 *) (p.bias + orow);
+                        floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
+                        if (p.out_scale) sc = *(const floatx4 *) (p.out_scale + (int64_t) fr * p.OC + orow);
+                        floatx4 v;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            v[j] = leaky(acc[a][b][i * 4 + j] * id[j] + bb[j]);
+                            if (p.out_scale) v[j] *= sc[j];
+                        }
+                        if constexpr (sizeof(TO) == 2) {
+                            half4 hv;
+#pragma unroll
+                            for (int j = 0; j < 4; j++) hv[j] = (half_t) v[j];
+                            *(half4 *) (smem + nl * ORS + ml * 2) = hv;
+                        } else {
+                            *(floatx4 *) (smem + nl * ORS + ml * 4) = v;
+                        }
+                    });
+                });
+            });
+        }
+        __syncthreads();
+        static_for<NCH / NT>([&](auto j) {
+            const int nq = tid / CPR + j * STEP;   // pixel of this pass
+            const int nl = h * BNP + nq;
+            const int y = y0 + nl / TW, x = x0 + nl % TW;
+            int64_t opix;
+            if constexpr (MODE == MODE_DENSE) opix = fr * HW + (int64_t) y * W + x;
+            else opix = fr * 4 * HW + (int64_t) (2 * y + (cls >> 1)) * (2 * W) + 2 * x + (cls & 1);
+            const u32x4 v = *(const u32x4 *) (smem + nq * ORS + mc * 16);
+            *(u32x4 *) (Yp + opix * p.OC + o) = v;
+        });
     });
 }
 
@@ -255,6 +270,13 @@ hipError_t launch_hfrag_nc(const ConvParams &p, int cfg, int mode, bool out_f16,
         if constexpr (NC == 16 && B == 128 && T_H == 16) {
             if (mode == MODE_SUBPIX) {
                 hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC, B, T_H, T_W, half_t, 4, 2>), grid,
+                                   dim3(256), 0, st, p, tiles_x, tiles_frame);
+                return hipGetLastError();
+            }
+        }
+        if constexpr (NC == 16 && B == 128) {
+            if (mode == MODE_DENSE && !out_f16) {
+                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_DENSE, NC, B, T_H, T_W, float, 4, 2>), grid,
                                    dim3(256), 0, st, p, tiles_x, tiles_frame);
                 return hipGetLastError();
             }
