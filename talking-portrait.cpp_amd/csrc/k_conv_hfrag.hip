@@ -25,7 +25,7 @@ static int hfrag_config(bool f16, int mode, int IC, int H, int W, int M) {
 bool modconv_hfrag_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, int W) {
     const int M = mode == MODE_DENSE ? OC : 4 * OC;
     const int cfg = hfrag_config(f16, mode, IC, H, W, M);
-    return cfg != 0 && (out_f16 || (mode == MODE_DENSE && cfg != 1));
+    return cfg != 0 && (out_f16 || (mode == MODE_DENSE && cfg != 1)) && (int64_t) M * 9 * IC * 2 < ((int64_t) 1 << 31);
 }
 
 TPMD_HFRAG_NC(1);
@@ -38,6 +38,8 @@ hipError_t launch_modconv_hfrag(ConvParams p, int mode, bool out_f16, hipStream_
     const int BM = cfg == 1 ? 256 : 128, TH = cfg == 3 ? 16 : 8, TW = cfg == 3 ? 16 : 32;
     const int64_t HW = (int64_t) p.H * p.W;
     if (p.N % HW != 0) return hipErrorInvalidValue;
+    // A is read through a buffer resource, whose extent is a 32-bit byte count
+    if ((int64_t) p.M * 9 * p.IC * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     p.MT = p.M / BM;
     p.T = 9 * p.IC / 32;
     const int tiles_x = p.W / TW, tiles_frame = tiles_x * (p.H / TH);

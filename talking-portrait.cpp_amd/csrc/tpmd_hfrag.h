@@ -92,10 +92,18 @@ __global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p
     const int MB = p.M / 32;
 
     // A fragment (tap, ks) of row block w = m0/32 + wm*TM + a: 1 KB at
-    // ((tap*KSA + ks)*MB + w) KB; this lane's 16 bytes of it
-    const TA *abase = (const TA *) p.A + ((int64_t) (m0 / 32 + wm * TM)) * 512 + lane * 8;
+    // ((tap*KSA + ks)*MB + w) KB; this lane's 16 bytes of it.
+    // A is read through a buffer resource: this lane's byte offset in the
+    // fragment is fixed (vector offset), the fragment's own offset is the
+    // same for every lane (scalar offset), so no per-load 64-bit address
+    // arithmetic runs on the VALU (measured at 16 frames: r64 / r128 / r256
+    // up-convs 141 / 151 / 168 -> 136 / 145 / 167 us beside the library)
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) p.A, (short) 0, (int) ((int64_t) p.M * 9 * IC * (int) sizeof(TA)), 0x00020000);
+    const unsigned avoff = (unsigned) (((m0 / 32 + wm * TM) * 512 + lane * 8) * (int) sizeof(TA));
     auto afrag = [&](int tap, int ks, int a) -> u32x4 {
-        return *(const u32x4 *) (abase + ((int64_t) (tap * KSA + ks) * MB + a) * 512);
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             ars, avoff, (int) (((tap * KSA + ks) * MB + a) * 1024), 0));
     };
     u32x4 af[3][TM][2];
     auto load_a = [&](int c, int tap, u32x4 (&dst)[TM][2]) {
