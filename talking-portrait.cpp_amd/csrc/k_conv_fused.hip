@@ -111,9 +111,15 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
     const int lrow = lane & 31, khalf = lane >> 5;
     // A fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
     u32x4 areg[3][KS];   // AREG: tap t's fragments in set t % 3, requested two taps ahead
-    const TA *afr = (const TA *) p.A + lane * 8;
+    // (through a buffer resource: this lane's byte offset fixed, the
+    // fragment's offset scalar)
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc((void *) p.A, (short) 0, (int) (C * K * 2), 0x00020000);
     auto load_a = [&](int tap, u32x4 (&dst)[KS]) {
-        static_for<KS>([&](auto s) { dst[s] = *(const u32x4 *) (afr + (tap * KS + s) * 512); });
+        static_for<KS>([&](auto s) {
+            dst[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   ars, (unsigned) (lane * 16), (int) ((tap * KS + s) * 1024), 0));
+        });
     };
     if constexpr (AREG) {
         load_a(0, areg[0]);
@@ -285,11 +291,20 @@ __global__ __launch_bounds__(256) void convh_tail_kernel(ConvParams p, TailArgs 
     // (t*KS + s)*MBK + mb); tap t's fragments go to register set t % 3
     const TA *Ab = (const TA *) p.A;
     const TA *arow = FRAG ? Ab + (mb * 64 + lane) * 8 : Ab + (int64_t) (mb * 32 + lrow) * K + khalf * 8;
+    // FRAG: through a buffer resource, this lane's byte offset fixed and the
+    // fragment's offset scalar
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc((void *) p.A, (short) 0, (int) (C * K * 2), 0x00020000);
+    const unsigned avoff = (unsigned) ((mb * 64 + lane) * 16);
     u32x4 af[3][KS];
     auto load_a = [&](int t, u32x4 (&dst)[KS]) {
         static_for<KS>([&](auto st) {
             constexpr int s = decltype(st)::value;
-            dst[s] = *(const u32x4 *) (arow + (FRAG ? (t * KS + s) * MBK * 512 : t * C + s * 16));
+            if constexpr (FRAG)
+                dst[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       ars, avoff, (int) ((t * KS + s) * MBK * 1024), 0));
+            else
+                dst[s] = *(const u32x4 *) (arow + t * C + s * 16);
         });
     };
 

@@ -57,9 +57,14 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_tail_kernel(ConvParams p
     const int n0 = (fr * H + y0) * W + x0;  // top-left pixel of the block
 
     // A fragment (tap, ks) of row block w = wm*TM + a: 1 KB at ((tap*KSA + ks)*MB + w) KB
-    const TA *abase = (const TA *) p.A + (wm * TM) * 512 + lane * 8;
+    // A through a buffer resource: this lane's byte offset fixed, the
+    // fragment's offset scalar (no VALU address arithmetic per load)
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc((void *) p.A, (short) 0, (int) (C * 9 * C * 2), 0x00020000);
+    const unsigned avoff = (unsigned) (((wm * TM) * 512 + lane * 8) * 2);
     auto afrag = [&](int tap, int ks, int a) -> u32x4 {
-        return *(const u32x4 *) (abase + ((tap * KSA + ks) * MB + a) * 512);
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             ars, avoff, (int) (((tap * KSA + ks) * MB + a) * 1024), 0));
     };
     u32x4 af[3][TM][2];
     auto load_a = [&](int c, int tap, u32x4 (&dst)[TM][2]) {
