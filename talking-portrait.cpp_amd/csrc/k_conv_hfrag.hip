@@ -38,8 +38,11 @@ hipError_t launch_modconv_hfrag(ConvParams p, int mode, bool out_f16, hipStream_
     const int BM = cfg == 1 ? 256 : 128, TH = cfg == 3 ? 16 : 8, TW = cfg == 3 ? 16 : 32;
     const int64_t HW = (int64_t) p.H * p.W;
     if (p.N % HW != 0) return hipErrorInvalidValue;
-    // A is read through a buffer resource, whose extent is a 32-bit byte count
-    if ((int64_t) p.M * 9 * p.IC * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    // A and the input are read through buffer resources, whose extents are
+    // 32-bit byte counts (a halo unit outside the map reads at 2^31)
+    if ((int64_t) p.M * 9 * p.IC * 2 >= ((int64_t) 1 << 31) ||
+        (p.N / HW) * p.x_bstride * 2 >= ((int64_t) 1 << 31))
+        return hipErrorInvalidValue;
     p.MT = p.M / BM;
     p.T = 9 * p.IC / 32;
     const int tiles_x = p.W / TW, tiles_frame = tiles_x * (p.H / TH);

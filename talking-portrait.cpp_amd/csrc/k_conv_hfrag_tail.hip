@@ -4,9 +4,6 @@
 
 namespace tpmd {
 
-// 16 zero bytes: the halo units outside the map read them
-__device__ __attribute__((aligned(16))) unsigned int hfrag_tail_zero16[4];
-
 // The conv (A fragments from L2, each 32-channel chunk's input halo in LDS,
 // chunk-major k) runs on 4 x 32 pixel blocks, 256 rows = every channel of the block, eight
 // waves of 64 rows x 64 pixels; the activated 256 x 128 tile then goes to LDS
@@ -71,23 +68,33 @@ __global__ __launch_bounds__(512) void modconv3x3_hfrag_tail_kernel(ConvParams p
         static_for<2>([&](auto s) { static_for<TM>([&](auto a) { dst[a][s] = afrag(tap, 2 * c + s, a); }); });
     };
 
-    // halo unit u = (wid*LPH + h)*64 + lane: halo pixel u / 5, chunk u % 5 (4: the pad)
-    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
-    const TA *hsrc[LPH];
-    bool hok[LPH];
+    // halo unit u = (wid*LPH + h)*64 + lane: halo pixel u / 5, chunk u % 5 (4: the pad),
+    // through a buffer resource over the input: this lane's unit's byte
+    // offset (past the extent for a unit outside the map, which the hardware
+    // answers with zeros) and the chunk's offset as the scalar offset
+    const int64_t xbytes = (int64_t) (p.N / (H * W)) * p.x_bstride * (int) sizeof(TA);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *) p.X, (short) 0, (int) xbytes, 0x00020000);
+    unsigned hvo[LPH];
 #pragma unroll
     for (int h = 0; h < LPH; h++) {
         const int u = (wid * LPH + h) * 64 + lane;
         const int hp = u / 5, q = u - hp * 5;
         const int hy = hp / HT_HWD, hx = hp - hy * HT_HWD;
         const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-        hok[h] = q < 4 && hp < HT_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
-        hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * C + q * 8 : Xf;
+        const bool ok = q < 4 && hp < HT_HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
+        hvo[h] = ok ? (unsigned) (((int64_t) fr * p.x_bstride + ((int64_t) iy * W + ix) * C + q * 8) *
+                                  (int) sizeof(TA))
+                    : 0x80000000u;
     }
-    const u32x4 *zero = (const u32x4 *) hfrag_tail_zero16;
+    // the halo goes through registers rather than the LDS DMA path: the
+    // compiler then counts every load exactly, while after an LDS DMA it
+    // waits for all loads in flight before the next MFMA
     u32x4 hreg[LPH];
     auto load_h = [&](int c) {
-        static_for<LPH>([&](auto h) { hreg[h] = *(hok[h] ? (const u32x4 *) (hsrc[h] + c * 32) : zero); });
+        static_for<LPH>([&](auto h) {
+            hreg[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, hvo[h], c * 64, 0));
+        });
     };
     auto store_h = [&](int c) {
         char *buf = smem + (c & 1) * HT_HBUF;
@@ -177,6 +184,8 @@ hipError_t launch_modconv_hfrag_tail(const ConvParams &p, const TailArgs &ta, bo
         return hipErrorInvalidValue;
     const int tiles_x = p.W / HT_TW, tiles_frame = tiles_x * (p.H / HT_TH);
     const int nframes = p.N / (p.H * p.W);
+    // the input is read through a buffer resource (32-bit byte extent)
+    if ((int64_t) nframes * p.x_bstride * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     const dim3 grid((unsigned) (nframes * tiles_frame));
     auto go = [&](auto c) {
         constexpr int CC = decltype(c)::value;

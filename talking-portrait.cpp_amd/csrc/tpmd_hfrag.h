@@ -7,10 +7,6 @@
 
 namespace tpmd {
 
-// 16 zero bytes: the halo units outside the map read them (one copy per
-// translation unit that instantiates the kernel)
-static __device__ __attribute__((aligned(16))) unsigned int halo_zero16[4];
-
 // Halo convs (f16 operands, every tile inside one frame): a tile is BM GEMM
 // rows x a TH x TW block of pixels of one frame, and the k order is
 // channel-chunk major, k tile t = c*9 + tap (32 channels c*32 .. +31 of tap
@@ -111,27 +107,33 @@ __global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p
     };
 
     // halo unit u = (wid*LPH + h)*64 + lane of a halo buffer: halo pixel u / 5,
-    // channel chunk u % 5 (4: the pad); units past the halo, pads and pixels
-    // outside the map read zeros
-    const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
-    const TA *hsrc[LPH];
-    bool hok[LPH];
+    // channel chunk u % 5 (4: the pad), read through a buffer resource over
+    // the input: the unit's byte offset as the vector offset (2^31, past the
+    // extent, for pads, units past the halo and pixels outside the map, which
+    // the hardware answers with zeros) and the chunk's offset as the scalar one
+    const int64_t xbytes = (int64_t) (p.N / (H * W)) * p.x_bstride * (int) sizeof(TA);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *) p.X, (short) 0, (int) xbytes, 0x00020000);
+    unsigned hvo[LPH];
 #pragma unroll
     for (int h = 0; h < LPH; h++) {
         const int u = (wid * LPH + h) * 64 + lane;
         const int hp = u / 5, q = u - hp * 5;
         const int hy = hp / HWD, hx = hp - hy * HWD;
         const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-        hok[h] = q < 4 && hp < HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
-        hsrc[h] = hok[h] ? Xf + ((int64_t) iy * W + ix) * IC + q * 8 : Xf;
+        const bool ok = q < 4 && hp < HPX && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
+        hvo[h] = ok ? (unsigned) (((int64_t) fr * p.x_bstride + ((int64_t) iy * W + ix) * IC + q * 8) *
+                                  (int) sizeof(TA))
+                    : 0x80000000u;
     }
     // the halo goes through registers rather than the LDS DMA path: the
     // compiler then counts every load exactly, while after an LDS DMA it
     // waits for all loads in flight before the next MFMA
-    const u32x4 *zero = (const u32x4 *) halo_zero16;
     u32x4 hreg[LPH];
     auto load_h = [&](int c) {
-        static_for<LPH>([&](auto h) { hreg[h] = *(hok[h] ? (const u32x4 *) (hsrc[h] + c * 32) : zero); });
+        static_for<LPH>([&](auto h) {
+            hreg[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, hvo[h], c * 64, 0));
+        });
     };
     auto store_h = [&](int c) {
         char *buf = smem + (c & 1) * HR_HBUF;
