@@ -105,6 +105,34 @@ __device__ __forceinline__ void upfirdn2x_load(const float *__restrict__ plane, 
         }
     }
 }
+// the same taps read through a buffer resource over the whole skip array:
+// plane0 = the plane's first element, 32-bit offsets instead of a 64-bit
+// address per tap
+__device__ __forceinline__ void upfirdn2x_load(__amdgpu_buffer_rsrc_t rs, unsigned plane0, int W, int H,
+                                               const float *__restrict__ k4, int X, int Y, upfirdn_taps &t) {
+    const int i0 = X & 1, j0 = Y & 1;
+    const int sx0 = (X + i0 - 2) >> 1, sy0 = (Y + j0 - 2) >> 1;
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++) {
+        const int sy = sy0 + jj;
+        const int cy = sy < 0 ? 0 : (sy >= H ? H - 1 : sy);
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++) {
+            const int sx = sx0 + ii;
+            const int cx = sx < 0 ? 0 : (sx >= W ? W - 1 : sx);
+            t.in[2 * jj + ii] = (unsigned) sy < (unsigned) H && (unsigned) sx < (unsigned) W;
+            t.v[2 * jj + ii] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rs, (plane0 + (unsigned) (cx + W * cy)) * 4u, 0, 0));
+            t.k[2 * jj + ii] = k4[i0 + 2 * ii + 4 * (j0 + 2 * jj)];
+        }
+    }
+}
+
+// buffer resource over `bytes` bytes at p (bytes < 2^31)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *) p, (short) 0, (int) bytes, 0x00020000);
+}
+
 __device__ __forceinline__ float upfirdn2x_sum(const upfirdn_taps &t) {
 #pragma clang fp contract(off)
     float acc = 0.0f;

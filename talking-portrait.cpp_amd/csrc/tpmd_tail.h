@@ -139,13 +139,15 @@ __device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int
         sk.lx = a.lin[x];
         sk.ly = a.lin[y];
         // every tap of the six planes is requested before any sum is formed
+        // (through buffer resources over the skip arrays: 32-bit offsets)
+        const int64_t sbytes = (int64_t) a.nframes * 3 * rh * rh * 4;
+        const __amdgpu_buffer_rsrc_t frs = buffer_rsrc(a.flow_prev, sbytes), rrs = buffer_rsrc(a.rgb_prev, sbytes);
         upfirdn_taps tf[3], tr[3];
 #pragma unroll
         for (int k = 0; k < 3; k++) {
-            if (a.flow_prev)
-                upfirdn2x_load(a.flow_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.fup, x, y, tf[k]);
-            if (a.rgb_prev)
-                upfirdn2x_load(a.rgb_prev + ((int64_t) fr * 3 + k) * rh * rh, rh, rh, a.rup, x, y, tr[k]);
+            const unsigned plane0 = (unsigned) ((fr * 3 + k) * rh * rh);
+            if (a.flow_prev) upfirdn2x_load(frs, plane0, rh, rh, a.fup, x, y, tf[k]);
+            if (a.rgb_prev) upfirdn2x_load(rrs, plane0, rh, rh, a.rup, x, y, tr[k]);
         }
         issue();
 #pragma unroll
@@ -215,6 +217,10 @@ template <typename T> struct feat8;
 template <> struct feat8<half_t> {
     half8 h;
     __device__ __forceinline__ void load(const half_t *p) { h = *(const half8 *) p; }
+    // at byte offset off of a buffer resource over the feature map
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, unsigned off) {
+        h = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
     __device__ __forceinline__ float operator[](int e) const { return (float) h[e]; }
 };
 template <> struct feat8<float> {
@@ -222,6 +228,10 @@ template <> struct feat8<float> {
     __device__ __forceinline__ void load(const float *p) {
         lo = *(const floatx4 *) p;
         hi = *(const floatx4 *) (p + 4);
+    }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, unsigned off) {
+        lo = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        hi = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u, 0, 0));
     }
     __device__ __forceinline__ float operator[](int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
 };
@@ -254,7 +264,8 @@ __device__ __forceinline__ void tail_flow_head(const TailArgs &a, float fl[3], i
 // map reads the zero pad after it.  Load the four taps' values ...
 __device__ __forceinline__ void tail_featg_load(const TailArgs &a, const taps4 &t, floatx4 gv[4]) {
     const int r = a.r, RR = r * r;
-    const char *gb = (const char *) a.featg;
+    // through a buffer resource over featg and its pad: 32-bit offsets
+    const __amdgpu_buffer_rsrc_t grs = buffer_rsrc(a.featg, (int64_t) RR * 16 + TAIL_FEATG_PAD);
     const unsigned gpad = (unsigned) RR * 16u;
     const bool inx[2] = {(unsigned) t.x0 < (unsigned) r, (unsigned) t.x0 + 1u < (unsigned) r};
     const bool iny[2] = {(unsigned) t.y0 < (unsigned) r, (unsigned) t.y0 + 1u < (unsigned) r};
@@ -262,7 +273,8 @@ __device__ __forceinline__ void tail_featg_load(const TailArgs &a, const taps4 &
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * 16);
-        gv[k] = *(const floatx4 *) (gb + (inx[k & 1] && iny[k >> 1] ? off : gpad));
+        gv[k] = __builtin_bit_cast(
+            floatx4, __builtin_amdgcn_raw_buffer_load_b128(grs, inx[k & 1] && iny[k >> 1] ? off : gpad, 0, 0));
     }
 }
 // ... then form and store the pixel's rgb
@@ -389,8 +401,8 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
     // 32-bit byte offsets from per-frame bases; a tap outside the map reads
     // the zero pad that follows the feature map (TAIL_FEAT_PAD bytes), whose
     // product w * 0 = +0 leaves the running sum unchanged, as skipping it does
-    const char *featb = (const char *) a.feat;
     const unsigned pad_off = (unsigned) RR * C * (unsigned) sizeof(TF);
+    const __amdgpu_buffer_rsrc_t featrs = buffer_rsrc(a.feat, (int64_t) pad_off + TAIL_FEAT_PAD);
     char *trunkb = a.trunk ? (char *) a.trunk + (int64_t) fr * RR * C * (int64_t) sizeof(TT) : nullptr;
     float *warpf = a.warp_tap ? a.warp_tap + (int64_t) fr * RR * C : nullptr;
     for (int it0 = 0; it0 < ITER; it0 += NB) {
@@ -412,7 +424,7 @@ __device__ __forceinline__ void tile_tail(const TailArgs &a, const float *so, fl
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const unsigned off = base + (unsigned) (((k >> 1) * r + (k & 1)) * C * (int) sizeof(TF));
-                fv[b][k].load((const TF *) (featb + (inx[k & 1] && iny[k >> 1] ? off : pad_off)));
+                fv[b][k].load(featrs, inx[k & 1] && iny[k >> 1] ? off : pad_off);
             }
         }
 #pragma unroll
