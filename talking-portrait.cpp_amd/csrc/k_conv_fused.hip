@@ -96,17 +96,7 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     u32x4 hv[PF];
     const tail_skip sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
-        static_for<PF>([&](auto i) {
-            const int ch = tid + i * NT;
-            hv[i] = u32x4{0u, 0u, 0u, 0u};
-            if (ch < HCH) {
-                const int px = ch / CPP, c = ch - px * CPP;
-                const int hy = px / HWD, hx = px - hy * HWD;
-                const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
-                    hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
-            }
-        });
+        halo_load<PF, NT, CPP, HWD, HCH, C>(Xf, H, W, y0, x0, tid, hv);
     });
     const int lrow = lane & 31, khalf = lane >> 5;
     // A fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
@@ -312,17 +302,7 @@ __global__ __launch_bounds__(256) void convh_tail_kernel(ConvParams p, TailArgs 
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     u32x4 hv[PF];
     const tail_skip sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
-        static_for<PF>([&](auto i) {
-            const int ch = tid + i * NT;
-            hv[i] = u32x4{0u, 0u, 0u, 0u};
-            if (ch < HCH) {
-                const int px = ch / CPP, c = ch - px * CPP;
-                const int hy = px / HWD, hx = px - hy * HWD;
-                const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-                if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
-                    hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * C + c * 8);
-            }
-        });
+        halo_load<PF, NT, CPP, HWD, HCH, C>(Xf, H, W, y0, x0, tid, hv);
     });
     load_a(0, af[0]);
     load_a(1, af[1]);
@@ -381,6 +361,8 @@ hipError_t launch_modconv_fused64(const ConvParams &p, const TailArgs &ta, bool 
                                   hipStream_t st) {
     constexpr int TH = fusedh_cfg<64>::TH;
     if (p.IC != 64 || p.OC != 64 || p.M != 64 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
+    // the input halo is read through a buffer resource over one frame (32-bit offsets)
+    if ((int64_t) p.H * p.W * p.IC * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));
@@ -408,6 +390,8 @@ hipError_t launch_modconv_fused32(const ConvParams &p, const TailArgs &ta, bool 
                                   hipStream_t st) {
     constexpr int TH = 16;
     if (p.IC != 32 || p.OC != 32 || p.M != 32 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
+    // the input halo is read through a buffer resource over one frame (32-bit offsets)
+    if ((int64_t) p.H * p.W * p.IC * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     const dim3 grid((unsigned) (nframes * tiles_frame));

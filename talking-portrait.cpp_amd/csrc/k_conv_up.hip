@@ -69,17 +69,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void u
     // halo -> registers, and the first tap's A fragments
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     u32x4 hv[PF];
-    static_for<PF>([&](auto i) {
-        const int ch = tid + i * NT;
-        hv[i] = u32x4{0u, 0u, 0u, 0u};
-        if (ch < HCH) {
-            const int px = ch / CPP, c = ch - px * CPP;
-            const int hy = px / HWD, hx = px - hy * HWD;
-            const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
-            if ((unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W)
-                hv[i] = *(const u32x4 *) (Xf + ((int64_t) iy * W + ix) * IC + c * 8);
-        }
-    });
+    halo_load<PF, NT, CPP, HWD, HCH, IC>(Xf, H, W, y0, x0, tid, hv);
     // A fragment (tap, step): rows 32*wid + lane%32, k = tap*IC + step*16 + (lane/32)*8 .. +8
     const TA *arow = FRAG ? (const TA *) p.A + (wid * 64 + lane) * 8
                           : (const TA *) p.A + (int64_t) (wid * 32 + lrow) * K + khalf * 8;
@@ -172,6 +162,8 @@ bool modconv_up64_ok(bool f16, bool out_f16, int mode, int IC, int OC, int H, in
 hipError_t launch_modconv_up64(const ConvParams &p, bool frag, hipStream_t st) {
     constexpr int TH = UP64_TH;
     if (p.IC != 64 || p.OC != 32 || p.M != 128 || p.W % 32 != 0 || p.H % TH != 0) return hipErrorInvalidValue;
+    // the input halo is read through a buffer resource over one frame (32-bit offsets)
+    if ((int64_t) p.H * p.W * p.IC * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     const int tiles_x = p.W / 32, tiles_frame = tiles_x * (p.H / TH);
     const int nframes = p.N / (p.H * p.W);
     if (frag)

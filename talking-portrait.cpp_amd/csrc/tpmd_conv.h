@@ -78,6 +78,27 @@ __device__ __forceinline__ int xcd_remap(int L, int total) {
     return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
+// Input halo of a TH x TW pixel block (top-left y0, x0) of one frame Xf
+// (channel-last, IC f16 channels, CPP = IC / 8 16-byte chunks per pixel,
+// HWD = TW + 2 halo pixels per row, HCH chunks in all) into registers: chunk
+// tid + i*NT of the halo in hv[i].  The loads go through a buffer resource
+// over the frame, so offsets are 32-bit and a pixel outside the map (or a
+// chunk past the halo) reads at an offset past the extent, which the hardware
+// answers with zeros: no branch and no 64-bit address per load.
+template <int PF, int NT, int CPP, int HWD, int HCH, int IC>
+__device__ __forceinline__ void halo_load(const half_t *Xf, int H, int W, int y0, int x0, int tid, u32x4 (&hv)[PF]) {
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(Xf, (int64_t) H * W * IC * 2);
+    static_for<PF>([&](auto i) {
+        const int ch = tid + i * NT;
+        const int px = ch / CPP, c = ch - px * CPP;
+        const int hy = px / HWD, hx = px - hy * HWD;
+        const int iy = y0 - 1 + hy, ix = x0 - 1 + hx;
+        const bool ok = ch < HCH && (unsigned) iy < (unsigned) H && (unsigned) ix < (unsigned) W;
+        const unsigned off = ok ? (unsigned) ((iy * W + ix) * IC * 2 + c * 16) : 0x80000000u;
+        hv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+    });
+}
+
 // activation of 4 consecutive GEMM rows m..m+3 of column n, stored to Y
 template <typename TO, int MODE>
 __device__ __forceinline__ void epi_store_quad(const ConvParams &p, const float acc[4], int m, int n) {

@@ -134,8 +134,18 @@ __device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int
     if (tid < BN) {
         const int r = a.r, rh = r >> 1, RR = r * r;
         const int fr = n0 / RR;
-        const int pix = tile_pix<TWC>(n0 - fr * RR, r, tid);
-        const int y = pix / r, x = pix - y * r;
+        const int pix0 = n0 - fr * RR;
+        int y, x;
+        if constexpr (TWC > 0) {
+            // the block's first row and column are the same for every lane
+            // (scalar division); the lane's offsets in the block follow
+            const int py0 = pix0 / r;
+            y = py0 + tid / TWC;
+            x = pix0 - py0 * r + tid % TWC;
+        } else {
+            y = (pix0 + tid) / r;
+            x = pix0 + tid - y * r;
+        }
         sk.lx = a.lin[x];
         sk.ly = a.lin[y];
         // every tap of the six planes is requested before any sum is formed
