@@ -29,6 +29,8 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", 
 
 SOURCES = ["k_gather.hip", "k_conv.hip", "k_conv_async.hip", "k_conv_hfrag.hip", "k_conv_hfrag8.hip", "k_conv_hfrag16.hip", "k_conv_hfrag_tail.hip", "k_conv_fused.hip", "k_conv_up.hip", "k_conv_halo.hip", "k_tail.hip", "k_style.hip", "k_enc.hip", "k_fmt.hip", "k_probe.hip", "tpmd.cpp", "tpme.cpp", "tpfm.cpp"]
 # plain C++ over the C ABI (no HIP): the tp::motion_dec shim, in the library
+# hipBLASLt: the FMT's f16 linear products (tpfm.cpp)
+LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 HOST_SOURCES = ["motion_dec.cpp", "motion_enc.cpp", "gguf.cpp", "gguf_abi.cpp"]
 CXX = os.environ.get("CXX", "g++")
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOSTDIR}"]
@@ -63,7 +65,7 @@ def build(verbose=False):
             if verbose and out.strip():
                 print(out)
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *LINK_LIBS])
     os.replace(tmp, LIB)
     # the shim's driver, linked against the library next to it
     tmp = SHIM_CHECK + ".tmp"

@@ -291,6 +291,13 @@ hipError_t launch_enc_conv(EncConvParams p, bool f16, hipStream_t st) {
     return hipGetLastError();
 }
 
+hipError_t launch_enc_epilogue(EncConvParams p, hipStream_t st) {
+    if (p.OC % 4 != 0 || p.OH < 1 || p.OW < 1 || !p.ws) return hipErrorInvalidValue;
+    p.ksplit = 1;
+    hipLaunchKernelGGL(enc_splitk_kernel, dim3(grid_1d((int64_t) p.OH * p.OW * (p.OC / 4))), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_enc_linear(const float *W, const float *b, const float *x, int O, int I, bool round16, float *y,
                              hipStream_t st) {
     hipLaunchKernelGGL(enc_linear_kernel, dim3((unsigned) ((O + 3) / 4)), dim3(256), 0, st, W, b, x, O, I,

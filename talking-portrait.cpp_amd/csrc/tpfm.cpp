@@ -1,16 +1,20 @@
 // Flow-matching transformer context behind the tpfm_* C ABI: the reference's
 // fmt_model (src/fmt.h:9-36) — weights, prepare, the CFG-batched forward
 // (src/fmt.cpp:44-205) — and its chunk sampler (src/pipeline.cpp:12-91), on
-// the k_fmt.hip kernels and the MFMA GEMM of k_enc.hip.  Host code only.
+// the k_fmt.hip kernels and the MFMA GEMM of k_enc.hip; the f16 linears'
+// products on hipBLASLt.  Host code only.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "tpmd_guard.h"
@@ -88,7 +92,41 @@ struct tpfm_ctx {
     float *tfk = nullptr, *tf = nullptr, *te0 = nullptr, *te = nullptr;
     float *cond_f = nullptr, *clin = nullptr, *x60 = nullptr, *x1 = nullptr, *x = nullptr;
     float *mod = nullptr, *qkv = nullptr, *v = nullptr;  // mod: [rows][mods.out]
-    float *ws = nullptr;  // split-K partials
+    float *ws = nullptr;  // split-K partials, or a library GEMM's f32 product
+
+    // The f16 linears (f16 weights and operand) run their product on hipBLASLt
+    // (f16 operands, f32 accumulation and output into ws) and the epilogue
+    // (bias, activation, adaLN gate, residual, operand copy) on the split-K
+    // pass of k_enc.hip.  180 token rows against up to 12.6 MB of weights
+    // leave the own 64 x 64 tile GEMM latency-bound (one forward's linears
+    // about 820 us with their split-K passes); the library's kernels for
+    // these shapes sum to about 290 us (measured in one graph on MI355X).
+    // A linear with only a bias after the product (qkv, the stacked adaLN
+    // layer, the final layer, the embedders) takes the bias in the library's
+    // epilogue and writes its f32 output directly (no epilogue pass).  One
+    // plan per (rows, out, in, direct), made at prepare; TPFM_BLASLT=0 keeps
+    // every linear on the own GEMM.
+    struct LtPlan {
+        hipblasLtMatmulDesc_t md = nullptr;
+        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
+        hipblasLtMatmulAlgo_t algo{};
+        size_t ws = 0;
+        bool bias = false;  // the library's epilogue adds a bias (direct plans)
+    };
+    hipblasLtHandle_t lt = nullptr;
+    void *lt_ws = nullptr;
+    static constexpr size_t LT_WS = (size_t) 32 << 20;
+    std::map<std::tuple<int, int, int, bool>, LtPlan> lt_plans;
+    void free_lt() {
+        for (auto &kv : lt_plans) {
+            if (kv.second.md) (void) hipblasLtMatmulDescDestroy(kv.second.md);
+            if (kv.second.la) (void) hipblasLtMatrixLayoutDestroy(kv.second.la);
+            if (kv.second.lb) (void) hipblasLtMatrixLayoutDestroy(kv.second.lb);
+            if (kv.second.ld) (void) hipblasLtMatrixLayoutDestroy(kv.second.ld);
+        }
+        lt_plans.clear();
+        lt_ws = nullptr;  // one of allocs
+    }
     void *cond_a = nullptr, *sc_a = nullptr, *x60_a = nullptr, *h_a = nullptr, *o_a = nullptr, *m1_a = nullptr;
 
     bool hip_ok(hipError_t e, const char *what) {
@@ -129,12 +167,14 @@ struct tpfm_ctx {
     }
     size_t asz(bool h) const { return h ? 2 : 4; }
     void free_all() {
+        free_lt();
         for (void *p : allocs) (void) hipFree(p);
         allocs.clear();
     }
     ~tpfm_ctx() {
         if (device >= 0) (void) hipSetDevice(device);
         free_all();
+        if (lt) (void) hipblasLtDestroy(lt);
         if (stream) (void) hipStreamDestroy(stream);
     }
 };
@@ -225,6 +265,66 @@ bool make_lin(tpfm_ctx *c, tpfm_ctx::Lin &L, const std::string &base, int out, i
     return make_lin_stack(c, L, {{base, out}}, in, in_pad);
 }
 
+// the hipBLASLt plan of an f16 linear over `rows` token rows, made once:
+// D (L.out x rows, column-major: [rows][L.out]) = W^T-stored-as-[L.in x L.out]^T
+// x X-stored-as-[L.in x rows], f16 operands, f32 accumulation and output
+// (into ws; direct: plus the f32 bias per output feature, into Y).  False
+// (and no plan) where the library has no kernel for the shape: that layer
+// keeps the own GEMM.
+bool lt_plan(tpfm_ctx *c, const tpfm_ctx::Lin &L, int rows, bool direct) {
+    const auto key = std::make_tuple(rows, L.out, L.in, direct);
+    if (c->lt_plans.count(key)) return true;
+    tpfm_ctx::LtPlan P;
+    bool ok = hipblasLtMatmulDescCreate(&P.md, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    ok = ok && hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS;
+    P.bias = direct && L.b;
+    if (P.bias) {
+        const hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
+        const hipDataType bt = HIP_R_32F;
+        const void *bp = L.b;
+        ok = ok &&
+             hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof ep) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof bp) ==
+                 HIPBLAS_STATUS_SUCCESS;
+    }
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.la, HIP_R_16F, L.in, L.out, L.in) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.lb, HIP_R_16F, L.in, rows, L.in) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.ld, HIP_R_32F, L.out, rows, L.out) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasLtMatmulHeuristicResult_t res{};
+    int n = 0;
+    if (ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS) {
+        const uint64_t wmax = tpfm_ctx::LT_WS;
+        ok = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax,
+                                                   sizeof wmax) == HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulAlgoGetHeuristic(c->lt, P.md, P.la, P.lb, P.ld, P.ld, pref, 1, &res, &n) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             n >= 1 && res.workspaceSize <= tpfm_ctx::LT_WS;
+        (void) hipblasLtMatmulPreferenceDestroy(pref);
+    } else {
+        ok = false;
+    }
+    if (ok) {
+        P.algo = res.algo;
+        P.ws = res.workspaceSize;
+    }
+    c->lt_plans[key] = P;  // destroyed with the others; an unusable plan is erased below
+    if (!ok) {
+        tpfm_ctx::LtPlan &Q = c->lt_plans[key];
+        if (Q.md) (void) hipblasLtMatmulDescDestroy(Q.md);
+        if (Q.la) (void) hipblasLtMatrixLayoutDestroy(Q.la);
+        if (Q.lb) (void) hipblasLtMatrixLayoutDestroy(Q.lb);
+        if (Q.ld) (void) hipblasLtMatrixLayoutDestroy(Q.ld);
+        c->lt_plans.erase(key);
+    }
+    return ok;
+}
+
 // y[rows][L.out] (+ gate, residual, activation, operand copy) = X[rows][L.in] L.W^T + L.b
 bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float *Y, void *Ya, bool ya16, int act,
             const float *gate = nullptr, int64_t gstride = 0, const float *res = nullptr) {
@@ -248,8 +348,37 @@ bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float 
     p.pad = 0;
     p.OH = 1;
     p.OW = rows;
-    p.ksplit = lin_splits(rows, L.out, L.in);
     p.ws = c->ws;
+    if (L.f16) {
+        // bias only, f32 output: the library's epilogue writes Y
+        const bool direct = Y && !Ya && act == 0 && !gate && !res;
+        auto it = c->lt_plans.find(std::make_tuple(rows, L.out, L.in, direct));
+        if (direct && (it == c->lt_plans.end() || it->second.bias != (L.b != nullptr)))
+            it = c->lt_plans.find(std::make_tuple(rows, L.out, L.in, false));
+        if (it != c->lt_plans.end()) {
+            const tpfm_ctx::LtPlan &P = it->second;
+            const bool dir = std::get<3>(it->first);
+            if (dir && P.bias) {
+                // the plan's shape is shared by layers with their own biases
+                const void *bp = L.b;
+                if (hipblasLtMatmulDescSetAttribute(P.md, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof bp) !=
+                    HIPBLAS_STATUS_SUCCESS) {
+                    c->err = "linear: setting the hipBLASLt bias pointer failed";
+                    return false;
+                }
+            }
+            float *D = dir ? Y : c->ws;
+            const float alpha = 1.0f, beta = 0.0f;
+            const hipblasStatus_t e = hipblasLtMatmul(c->lt, P.md, &alpha, L.W, P.la, X, P.lb, &beta, D, P.ld, D,
+                                                      P.ld, &P.algo, c->lt_ws, P.ws, c->stream);
+            if (e != HIPBLAS_STATUS_SUCCESS) {
+                c->err = ffmt("linear: hipblasLtMatmul failed (status %d)", (int) e);
+                return false;
+            }
+            return dir || c->hip_ok(launch_enc_epilogue(p, c->stream), "linear epilogue");
+        }
+    }
+    p.ksplit = lin_splits(rows, L.out, L.in);
     return c->hip_ok(launch_enc_conv(p, L.f16, c->stream), "linear");
 }
 
@@ -472,9 +601,13 @@ static int tpfm_prepare_body(tpfm_ctx *c) {
     c->v = F((size_t) R * g.dim_w);
     {
         size_t wsn = 1;
+        // f16 linears may run their product on hipBLASLt into ws
+        const char *ev = getenv("TPFM_BLASLT");
+        const bool use_lt = c->f16 && !(ev && ev[0] == '0');
         auto need_ws = [&](const tpfm_ctx::Lin &L, int rows) {
             const int k = lin_splits(rows, L.out, L.in);
             if (k > 1) wsn = std::max(wsn, (size_t) k * rows * L.out);
+            if (use_lt && L.f16) wsn = std::max(wsn, (size_t) rows * L.out);
         };
         need_ws(c->cemb, R);
         need_ws(c->xemb, T);
@@ -487,6 +620,28 @@ static int tpfm_prepare_body(tpfm_ctx *c) {
             need_ws(B.fc2, R);
         }
         c->ws = F(wsn);
+        if (use_lt) {
+            if (!c->lt && hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
+                c->lt = nullptr;
+                c->err = "hipblasLtCreate failed";
+                return -1;
+            }
+            c->lt_ws = c->dalloc(tpfm_ctx::LT_WS);
+            if (!c->lt_ws) return -1;
+            auto plan = [&](const tpfm_ctx::Lin &L, int rows, bool direct) {
+                if (L.f16) (void) lt_plan(c, L, rows, direct);
+            };
+            plan(c->cemb, R, true);
+            plan(c->xemb, T, true);
+            plan(c->mods, R, true);
+            plan(c->fin_lin, R, true);
+            for (const auto &B : c->blocks) {
+                plan(B.qkv, R, true);
+                plan(B.proj, R, false);
+                plan(B.fc1, R, false);
+                plan(B.fc2, R, false);
+            }
+        }
     }
     c->h_cond.assign((size_t) 3 * T * c->CD, 0.0f);
     c->h_x60.assign((size_t) T * g.dim_w, 0.0f);

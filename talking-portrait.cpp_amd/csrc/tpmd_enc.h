@@ -30,6 +30,9 @@ hipError_t launch_enc_stem(const float *img, const float *w, const float *b, int
 hipError_t launch_enc_blur(const float *x, const float *k, int H, int W, int C, int pad, void *y, bool y_f16,
                            hipStream_t st);
 hipError_t launch_enc_conv(EncConvParams p, bool f16, hipStream_t st);
+// the conv's epilogue alone, on the f32 product [OH*OW][OC] already in p.ws
+// (p.ksplit ignored): bias, activation, gate, residual, Y and Ya as above
+hipError_t launch_enc_epilogue(EncConvParams p, hipStream_t st);
 hipError_t launch_enc_linear(const float *W, const float *b, const float *x, int O, int I, bool round16, float *y,
                              hipStream_t st);
 
