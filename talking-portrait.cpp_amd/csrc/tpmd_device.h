@@ -105,11 +105,39 @@ __device__ __forceinline__ void upfirdn2x_load(const float *__restrict__ plane, 
         }
     }
 }
-// the same taps read through a buffer resource over the whole skip array:
+// the four kernel taps output (X, Y) uses, in upfirdn_taps order: the 16
+// taps are the same for every lane (scalar loads), the lane's four follow
+// from its output parity by selects, so planes that share the kernel share
+// them and no lane issues a vector load for a weight
+struct upfirdn_k {
+    float k[4];
+};
+__device__ __forceinline__ upfirdn_k upfirdn2x_weights(const float *__restrict__ k4, int X, int Y) {
+    // (read through the constant address space: a uniform address there is
+    // a scalar load; the kernel is never written while a launch runs.  The
+    // taps are named values, not an array, and pass through readfirstlane,
+    // so the selects stay register selects instead of being folded into an
+    // indexed private array)
+    const __attribute__((address_space(4))) float *kc = (const __attribute__((address_space(4))) float *) k4;
+    auto sk = [&](int q) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(kc[q]))); };
+    const float k0 = sk(0), k1 = sk(1), k2 = sk(2), k3 = sk(3), k4_ = sk(4), k5 = sk(5), k6 = sk(6), k7 = sk(7);
+    const float k8 = sk(8), k9 = sk(9), k10 = sk(10), k11 = sk(11), k12 = sk(12), k13 = sk(13), k14 = sk(14),
+                k15 = sk(15);
+    const bool i1 = X & 1, j1 = Y & 1;
+    // tap (ii, jj) is k4[i0 + 2*ii + 4*(j0 + 2*jj)]: of b, b+1, b+4, b+5 with b = 2*ii + 8*jj
+    auto pick = [&](float kb, float kb1, float kb4, float kb5) { return j1 ? (i1 ? kb5 : kb4) : (i1 ? kb1 : kb); };
+    upfirdn_k r;
+    r.k[0] = pick(k0, k1, k4_, k5);
+    r.k[1] = pick(k2, k3, k6, k7);
+    r.k[2] = pick(k8, k9, k12, k13);
+    r.k[3] = pick(k10, k11, k14, k15);
+    return r;
+}
+// the data taps read through a buffer resource over the whole skip array:
 // plane0 = the plane's first element, 32-bit offsets instead of a 64-bit
-// address per tap
+// address per tap; the kernel taps from upfirdn2x_weights
 __device__ __forceinline__ void upfirdn2x_load(__amdgpu_buffer_rsrc_t rs, unsigned plane0, int W, int H,
-                                               const float *__restrict__ k4, int X, int Y, upfirdn_taps &t) {
+                                               const upfirdn_k &kw, int X, int Y, upfirdn_taps &t) {
     const int i0 = X & 1, j0 = Y & 1;
     const int sx0 = (X + i0 - 2) >> 1, sy0 = (Y + j0 - 2) >> 1;
 #pragma unroll
@@ -123,7 +151,7 @@ __device__ __forceinline__ void upfirdn2x_load(__amdgpu_buffer_rsrc_t rs, unsign
             t.in[2 * jj + ii] = (unsigned) sy < (unsigned) H && (unsigned) sx < (unsigned) W;
             t.v[2 * jj + ii] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rs, (plane0 + (unsigned) (cx + W * cy)) * 4u, 0, 0));
-            t.k[2 * jj + ii] = k4[i0 + 2 * ii + 4 * (j0 + 2 * jj)];
+            t.k[2 * jj + ii] = kw.k[2 * jj + ii];
         }
     }
 }

@@ -152,12 +152,16 @@ __device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int
         // (through buffer resources over the skip arrays: 32-bit offsets)
         const int64_t sbytes = (int64_t) a.nframes * 3 * rh * rh * 4;
         const __amdgpu_buffer_rsrc_t frs = buffer_rsrc(a.flow_prev, sbytes), rrs = buffer_rsrc(a.rgb_prev, sbytes);
+        // the kernel taps once per kernel, shared by its three planes
+        upfirdn_k kf{}, kr{};
+        if (a.flow_prev) kf = upfirdn2x_weights(a.fup, x, y);
+        if (a.rgb_prev) kr = upfirdn2x_weights(a.rup, x, y);
         upfirdn_taps tf[3], tr[3];
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             const unsigned plane0 = (unsigned) ((fr * 3 + k) * rh * rh);
-            if (a.flow_prev) upfirdn2x_load(frs, plane0, rh, rh, a.fup, x, y, tf[k]);
-            if (a.rgb_prev) upfirdn2x_load(rrs, plane0, rh, rh, a.rup, x, y, tr[k]);
+            if (a.flow_prev) upfirdn2x_load(frs, plane0, rh, rh, kf, x, y, tf[k]);
+            if (a.rgb_prev) upfirdn2x_load(rrs, plane0, rh, rh, kr, x, y, tr[k]);
         }
         issue();
 #pragma unroll
