@@ -60,7 +60,12 @@ struct fused32_cfg {
     static constexpr int AOFF = (HALO + 255) / 256 * 256;  // A fragments, fragment-major
     static constexpr int CONV = AOFF + (AREG ? 0 : NAF * 1024);  // conv-phase LDS
     static constexpr int TAIL = FG ? 0 : L::WFS0 * 4;       // so + prm, over the conv's LDS
-    static constexpr int WFS = CONV > TAIL ? CONV : TAIL;
+    // FG: the block's skip windows after the halo (after A when A sits in
+    // LDS), then the ToFlow weights: 53.7 KB with A in registers, three
+    // workgroups per CU at any LDS allocation granule up to 1280 bytes
+    typedef skip_lds<TH, TW, NT> SK;
+    static constexpr int SKOFF = FG ? (AREG ? (HALO + 15) / 16 * 16 : CONV) : 0;
+    static constexpr int WFS = FG ? SKOFF + SK::FLOATS * 4 : (CONV > TAIL ? CONV : TAIL);
     static constexpr int LDS = WFS + 3 * C * 4;
     static_assert(TH % (NT / 64) == 0 && (FG ? BN == NT : BN % NT == 0), "rows per wave");
     static_assert(!FG || RPW == 2, "FG: a lane's two block rows are its pixel and its partner's");
@@ -92,12 +97,24 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
 
     // memory order, bounded by registers: the tail's skips and the halo are
     // requested together; once the skips are summed (the halo still in
-    // flight) the A fragments and the frame's ToFlow weights follow
+    // flight) the A fragments and the frame's ToFlow weights follow.  FG: the
+    // block's skip windows go to LDS with the halo instead (a few values per
+    // thread), and each pixel sums its skips after the conv
     const TA *Xf = (const TA *) p.X + (int64_t) fr * p.x_bstride;
     u32x4 hv[PF];
-    const tail_skip sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
+    tail_skip sk{};
+    float skv[F::SK::NV];
+    float lx = 0.0f, ly = 0.0f;
+    if constexpr (FG) {
+        skip_window_load<TH, TW, NT>(ta, fr, y0, x0, tid, skv);
+        lx = ta.lin[x0 + tid % TW];
+        ly = ta.lin[y0 + tid / TW];
         halo_load<PF, NT, CPP, HWD, HCH, C>(Xf, H, W, y0, x0, tid, hv);
-    });
+    } else {
+        sk = tile_tail_skips_then<BN, TW>(ta, n0, tid, [&]() {
+            halo_load<PF, NT, CPP, HWD, HCH, C>(Xf, H, W, y0, x0, tid, hv);
+        });
+    }
     const int lrow = lane & 31, khalf = lane >> 5;
     // A fragment f = tap*KS + step: lane l holds A[l%32][f*16 + (l/32)*8 .. +8]
     u32x4 areg[3][KS];   // AREG: tap t's fragments in set t % 3, requested two taps ahead
@@ -130,6 +147,7 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
         }
     });
     tile_tail_wfs_store<C, NT>(wfs, tid, wr);
+    if constexpr (FG) skip_window_store<TH, TW, NT>((float *) (smem + F::SKOFF), tid, skv);
     __syncthreads();  // (waits for the A fragments' DMA too, when A goes through LDS)
 
     // conv: acc[b] = 32 channels x the 32 pixels of output row wid*RPW + b
@@ -191,10 +209,13 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
             fl[k] = khalf ? got + mine : mine + got;
         }
         const int pix = tile_pix<TW>(n0 - fr * (H * W), W, tid);
+        const tail_skip skw =
+            skip_from_window<TH, TW, NT>(ta, (const float *) (smem + F::SKOFF), y0, x0, x0 + tid % TW, y0 + tid / TW,
+                                         lx, ly);
         taps4 t;
         float m;
-        tail_flow_head(ta, fl, fr, pix, sk, t, m);
-        tail_featg_rgb(ta, t, m, fr, pix, sk);
+        tail_flow_head(ta, fl, fr, pix, skw, t, m);
+        tail_featg_rgb(ta, t, m, fr, pix, skw);
         return;
     }
     __syncthreads();  // halo reads done: the LDS becomes the activated tile

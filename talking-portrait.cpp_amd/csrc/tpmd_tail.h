@@ -175,6 +175,101 @@ __device__ __forceinline__ tail_skip tile_tail_skips_then(const TailArgs &a, int
     return sk;
 }
 
+// The skips of a whole TH x TW output block (TH, TW even; top-left y0, x0
+// even) staged in LDS: the 2x upfirdn taps of its pixels lie in rows
+// y0/2 - 1 .. y0/2 + TH/2 and columns x0/2 - 1 .. x0/2 + TW/2 of the
+// half-resolution planes, SKH x SKW values per plane (source indices clamped
+// into the plane, as upfirdn2x_load clamps them; a tap outside the plane is
+// skipped by the sum all the same).  The workgroup requests the six planes'
+// windows together, one value per thread and step (instead of 24 single
+// loads per pixel, most of them shared with the neighbours), stores them
+// with the halo, and each pixel reads its taps back when it needs them:
+// the same values summed in the same order as tile_tail_skips.
+template <int TH, int TW, int NT>
+struct skip_lds {
+    static constexpr int SKH = TH / 2 + 2, SKW = TW / 2 + 2, PL = SKH * SKW;
+    static constexpr int FLOATS = 6 * PL;            // flow planes 0-2, rgb planes 3-5
+    static constexpr int NV = (FLOATS + NT - 1) / NT;  // values per thread
+};
+template <int TH, int TW, int NT>
+__device__ __forceinline__ void skip_window_load(const TailArgs &a, int fr, int y0, int x0, int tid,
+                                                 float (&v)[skip_lds<TH, TW, NT>::NV]) {
+    typedef skip_lds<TH, TW, NT> S;
+    const int rh = a.r >> 1;
+    const int64_t sbytes = (int64_t) a.nframes * 3 * rh * rh * 4;
+    const __amdgpu_buffer_rsrc_t frs = buffer_rsrc(a.flow_prev, sbytes), rrs = buffer_rsrc(a.rgb_prev, sbytes);
+#pragma unroll
+    for (int j = 0; j < S::NV; j++) {
+        const int i = tid + j * NT;
+        const int pl = i / S::PL, rem = i - pl * S::PL;
+        const int wr = rem / S::SKW, wc = rem - wr * S::SKW;
+        int sy = (y0 >> 1) - 1 + wr, sx = (x0 >> 1) - 1 + wc;
+        sy = sy < 0 ? 0 : (sy >= rh ? rh - 1 : sy);
+        sx = sx < 0 ? 0 : (sx >= rh ? rh - 1 : sx);
+        const int k = pl < 3 ? pl : pl - 3;
+        const unsigned off = (unsigned) (((fr * 3 + k) * rh + sy) * rh + sx) * 4u;
+        // past the extent (zeros) for the steps past the six windows and for absent skips
+        const bool rgb = pl >= 3;
+        const bool have = i < S::FLOATS && (rgb ? a.rgb_prev != nullptr : a.flow_prev != nullptr);
+        const unsigned o = have ? off : 0x80000000u;
+        v[j] = rgb ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rrs, o, 0, 0))
+                   : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(frs, o, 0, 0));
+    }
+}
+template <int TH, int TW, int NT>
+__device__ __forceinline__ void skip_window_store(float *lds, int tid, const float (&v)[skip_lds<TH, TW, NT>::NV]) {
+    typedef skip_lds<TH, TW, NT> S;
+#pragma unroll
+    for (int j = 0; j < S::NV; j++) {
+        const int i = tid + j * NT;
+        if (i < S::FLOATS) lds[i] = v[j];
+    }
+}
+// the skips of output pixel (x, y) of the block from the staged windows;
+// lx, ly: its identity-grid coordinates lin[x], lin[y] (loaded earlier)
+template <int TH, int TW, int NT>
+__device__ __forceinline__ tail_skip skip_from_window(const TailArgs &a, const float *lds, int y0, int x0, int x,
+                                                      int y, float lx, float ly) {
+#pragma clang fp contract(off)
+    typedef skip_lds<TH, TW, NT> S;
+    tail_skip sk;
+#pragma unroll
+    for (int k = 0; k < 3; k++) sk.fl[k] = sk.rgb[k] = 0.0f;
+    sk.lx = lx;
+    sk.ly = ly;
+    const int rh = a.r >> 1;
+    const int i0 = x & 1, j0 = y & 1;
+    const int sx0 = (x + i0 - 2) >> 1, sy0 = (y + j0 - 2) >> 1;
+    const int w0 = (sy0 - ((y0 >> 1) - 1)) * S::SKW + sx0 - ((x0 >> 1) - 1);  // window index of tap (0, 0)
+    bool in[4];
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++)
+            in[2 * jj + ii] = (unsigned) (sy0 + jj) < (unsigned) rh && (unsigned) (sx0 + ii) < (unsigned) rh;
+    auto plane = [&](int pl, const upfirdn_k &kw) {
+        upfirdn_taps t;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            t.v[q] = lds[pl * S::PL + w0 + (q >> 1) * S::SKW + (q & 1)];
+            t.k[q] = kw.k[q];
+            t.in[q] = in[q];
+        }
+        return upfirdn2x_sum(t);
+    };
+    if (a.flow_prev) {
+        const upfirdn_k kf = upfirdn2x_weights(a.fup, x, y);
+#pragma unroll
+        for (int k = 0; k < 3; k++) sk.fl[k] = plane(k, kf);
+    }
+    if (a.rgb_prev) {
+        const upfirdn_k kr = upfirdn2x_weights(a.rup, x, y);
+#pragma unroll
+        for (int k = 0; k < 3; k++) sk.rgb[k] = plane(3 + k, kr);
+    }
+    return sk;
+}
+
 // park tile pixel tid's skips in its LDS record (prm, [BN][8] floats) while
 // the conv runs, and take them back before phase 1 overwrites the record
 template <int BN>
