@@ -186,8 +186,18 @@ __global__ __launch_bounds__(F32_NT) __attribute__((amdgpu_waves_per_eu(6))) voi
         });
         static_for<4>([&](auto i) {
             const int row = i * 8 + khalf * 4;
-            const floatx4 id = *(const floatx4 *) (p.inv_den + (int64_t) fr * C + row);
-            const floatx4 bb = *(const floatx4 *) (p.bias + row);
+            // 1/den and bias of the frame's channels as scalar loads, each
+            // lane half taking its four: no vector load (and no memory
+            // round trip) after the conv
+            floatx4 id, bb;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float d0 = ld_uniform(p.inv_den + (int64_t) fr * C, i * 8 + j);
+                const float d1 = ld_uniform(p.inv_den + (int64_t) fr * C, i * 8 + 4 + j);
+                const float b0 = ld_uniform(p.bias, i * 8 + j), b1 = ld_uniform(p.bias, i * 8 + 4 + j);
+                id[j] = khalf ? d1 : d0;
+                bb[j] = khalf ? b1 : b0;
+            }
             floatx4 w[3];
 #pragma unroll
             for (int k = 0; k < 3; k++) w[k] = *(const floatx4 *) (wfs + k * C + row);

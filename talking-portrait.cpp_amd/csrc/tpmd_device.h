@@ -156,6 +156,15 @@ __device__ __forceinline__ void upfirdn2x_load(__amdgpu_buffer_rsrc_t rs, unsign
     }
 }
 
+// p[i] for a uniform p and i as a scalar load (through the constant address
+// space; the data is never written while a launch runs), kept a register
+// value by readfirstlane so that selects between such values are not folded
+// into a vector load at a per-lane address
+__device__ __forceinline__ float ld_uniform(const float *p, int i) {
+    const __attribute__((address_space(4))) float *c = (const __attribute__((address_space(4))) float *) p;
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c[i])));
+}
+
 // buffer resource over `bytes` bytes at p (bytes < 2^31)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *) p, (short) 0, (int) bytes, 0x00020000);

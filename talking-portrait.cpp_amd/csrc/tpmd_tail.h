@@ -355,7 +355,7 @@ __device__ __forceinline__ void tail_flow_head(const TailArgs &a, float fl[3], i
     const int r = a.r, RR = r * r;
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-        fl[k] = fl[k] + a.fbias[k];
+        fl[k] = fl[k] + ld_uniform(a.fbias, k);
         if (a.flow_prev) fl[k] = fl[k] + sk.fl[k];
     }
     if (a.flow_cur) {
@@ -401,8 +401,8 @@ __device__ __forceinline__ void tail_featg_finish(const TailArgs &a, const taps4
     float *rgbf = a.rgb_cur + (int64_t) fr * 3 * RR;
 #pragma unroll
     for (int q = 0; q < 3; q++) {
-        float v = leaky(rgb[q] * m + a.rlb[q]);
-        v = v + a.rbias[q];
+        float v = leaky(rgb[q] * m + ld_uniform(a.rlb, q));
+        v = v + ld_uniform(a.rbias, q);
         if (a.rgb_prev) v = v + skr[q];
         rgbf[(unsigned) (q * RR + pix)] = v;
     }
