@@ -344,7 +344,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(frames shard across GPUs with no per-frame collective; see DESIGN.md)",
+              "(frames shard across GPUs by batch, with no collective per frame)",
               file=sys.stderr)
         sys.exit(2)
 
