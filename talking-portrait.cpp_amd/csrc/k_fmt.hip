@@ -7,7 +7,8 @@
 //   fmt_silu_kernel      in place, the t-embedder's hidden layer
 //   fmt_cond_kernel      silu(c_embed + t_embed) in the adaLN GEMMs' operand type
 //   fmt_xpos_kernel      x = x_embed + pos, replicated over the CFG branches
-//   fmt_ln_mod_kernel    LayerNorm (no affine) then adaLN modulate: n*scale + n + shift
+//   fmt_ln_mod_kernel    LayerNorm (no affine) then adaLN modulate: n*scale + n + shift,
+//                        optionally after the gated residual update of the linear before it
 //   fmt_attn_kernel      banded multi-head attention (softmax(q k / sqrt(hd) + mask) v)
 //   fmt_euler_kernel     CFG combination of the three branches and the Euler step
 #include "tpmd_conv.h"
@@ -70,10 +71,17 @@ __global__ __launch_bounds__(256) void fmt_xpos_kernel(const float *__restrict__
 // one workgroup per row of H: mean, then the variance of the centred values
 // (two passes over registers), n = (x - mean) / sqrt(var + eps),
 // h = n * scale + n + shift
-template <typename TO>
-__global__ __launch_bounds__(256) void fmt_ln_mod_kernel(const float *__restrict__ x, const float *__restrict__ mod,
+// RES: first the residual update of the linear before it, whose f32
+// product P (no bias) is given: x += gate * (P + b), stored back to x, as
+// the linear's own epilogue pass computes it; then the norm of the new x
+template <typename TO, bool RES>
+// (x and xout alias: RES updates x in place, each element read and then
+// written by one thread)
+__global__ __launch_bounds__(256) void fmt_ln_mod_kernel(const float *x, const float *__restrict__ mod,
                                                          int64_t mstride, int shift_off, int scale_off, int H,
-                                                         float eps, TO *__restrict__ y) {
+                                                         float eps, TO *__restrict__ y, const float *__restrict__ prod,
+                                                         const float *__restrict__ bias, const float *__restrict__ gate,
+                                                         int64_t gstride, float *xout) {
     constexpr int MAXV = 16;  // H <= 4096
     __shared__ float red[4];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -84,6 +92,15 @@ __global__ __launch_bounds__(256) void fmt_ln_mod_kernel(const float *__restrict
     for (int k = 0; k < MAXV; k++) {
         const int i = tid + k * 256;
         v[k] = i < H ? xr[i] : 0.0f;
+        if constexpr (RES) {
+            if (i < H) {
+                float a = prod[(int64_t) row * H + i];
+                if (bias) a = a + bias[i];
+                a = gate[(int64_t) row * gstride + i] * a;
+                v[k] = v[k] + a;
+                xout[(int64_t) row * H + i] = v[k];
+            }
+        }
         s += v[k];
     }
     auto block_sum = [&](float a) {
@@ -235,11 +252,24 @@ hipError_t launch_fmt_ln_mod(const float *x, const float *mod, int64_t mstride, 
                              int rows, int H, float eps, void *y, bool f16, hipStream_t st) {
     if (H > 16 * 256) return hipErrorInvalidValue;
     if (f16)
-        hipLaunchKernelGGL(fmt_ln_mod_kernel<half_t>, dim3((unsigned) rows), dim3(256), 0, st, x, mod, mstride,
-                           shift_off, scale_off, H, eps, (half_t *) y);
+        hipLaunchKernelGGL((fmt_ln_mod_kernel<half_t, false>), dim3((unsigned) rows), dim3(256), 0, st, x, mod,
+                           mstride, shift_off, scale_off, H, eps, (half_t *) y, nullptr, nullptr, nullptr, 0, nullptr);
     else
-        hipLaunchKernelGGL(fmt_ln_mod_kernel<float>, dim3((unsigned) rows), dim3(256), 0, st, x, mod, mstride,
-                           shift_off, scale_off, H, eps, (float *) y);
+        hipLaunchKernelGGL((fmt_ln_mod_kernel<float, false>), dim3((unsigned) rows), dim3(256), 0, st, x, mod,
+                           mstride, shift_off, scale_off, H, eps, (float *) y, nullptr, nullptr, nullptr, 0, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_fmt_res_ln_mod(const float *prod, const float *bias, const float *gate, int64_t gstride, float *x,
+                                 const float *mod, int64_t mstride, int shift_off, int scale_off, int rows, int H,
+                                 float eps, void *y, bool f16, hipStream_t st) {
+    if (H > 16 * 256 || !prod || !gate || !x) return hipErrorInvalidValue;
+    if (f16)
+        hipLaunchKernelGGL((fmt_ln_mod_kernel<half_t, true>), dim3((unsigned) rows), dim3(256), 0, st, x, mod,
+                           mstride, shift_off, scale_off, H, eps, (half_t *) y, prod, bias, gate, gstride, x);
+    else
+        hipLaunchKernelGGL((fmt_ln_mod_kernel<float, true>), dim3((unsigned) rows), dim3(256), 0, st, x, mod,
+                           mstride, shift_off, scale_off, H, eps, (float *) y, prod, bias, gate, gstride, x);
     return hipGetLastError();
 }
 

@@ -382,6 +382,23 @@ bool linear(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows, float 
     return c->hip_ok(launch_enc_conv(p, L.f16, c->stream), "linear");
 }
 
+// the f32 product X W^T of an f16 linear into ws on its hipBLASLt plan (no
+// bias, no epilogue): 1 done, 0 the layer has no plan, -1 error
+int lt_product(tpfm_ctx *c, const tpfm_ctx::Lin &L, const void *X, int rows) {
+    if (!L.f16) return 0;
+    const auto it = c->lt_plans.find(std::make_tuple(rows, L.out, L.in, false));
+    if (it == c->lt_plans.end()) return 0;
+    const tpfm_ctx::LtPlan &P = it->second;
+    const float alpha = 1.0f, beta = 0.0f;
+    const hipblasStatus_t e = hipblasLtMatmul(c->lt, P.md, &alpha, L.W, P.la, X, P.lb, &beta, c->ws, P.ld, c->ws,
+                                              P.ld, &P.algo, c->lt_ws, P.ws, c->stream);
+    if (e != HIPBLAS_STATUS_SUCCESS) {
+        c->err = ffmt("linear: hipblasLtMatmul failed (status %d)", (int) e);
+        return -1;
+    }
+    return 1;
+}
+
 // c_embed(cond) into clin, from the condition rows in cond_a: the same for
 // every ODE step of a chunk, so it runs once per chunk
 bool enqueue_cond_embed(tpfm_ctx *c) {
@@ -412,29 +429,49 @@ bool enqueue_forward(tpfm_ctx *c, float t) {
     // all adaLN modulations at once: block i's shift/scale/gate at columns 6H i .. of mod
     const int64_t ms = c->mods.out;
     if (!linear(c, c->mods, c->sc_a, R, c->mod, nullptr, false, 0)) return false;
+    const float *fmd = c->mod + c->blocks.size() * 6 * (size_t) H;  // the final layer's shift / scale
+    // x += gate * (X L.W^T + L.b), then h_a = modulate(norm(x)) with the
+    // shift / scale at columns sh, sc of nmd: one launch after the library
+    // product, or the linear's own epilogue and the norm
+    auto residual_norm = [&](const tpfm_ctx::Lin &L, const void *X, const float *gate, const float *nmd, int sh,
+                             int sc, bool out16) -> bool {
+        const int r = lt_product(c, L, X, R);
+        if (r < 0) return false;
+        if (r == 1)
+            return c->hip_ok(launch_fmt_res_ln_mod(c->ws, L.b, gate, ms, c->x, nmd, ms, sh, sc, R, H, g.ln_eps,
+                                                   c->h_a, out16, st),
+                             "residual + norm");
+        return linear(c, L, X, R, c->x, nullptr, false, 0, gate, ms, c->x) &&
+               c->hip_ok(launch_fmt_ln_mod(c->x, nmd, ms, sh, sc, R, H, g.ln_eps, c->h_a, out16, st), "norm");
+    };
+    // the first block's attention norm (the later norms follow the residual
+    // updates that precede them)
+    if (!c->blocks.empty() &&
+        !c->hip_ok(launch_fmt_ln_mod(c->x, c->mod, ms, 0, H, R, H, g.ln_eps, c->h_a, c->blocks[0].qkv.f16, st),
+                   "norm"))
+        return false;
     for (size_t i = 0; i < c->blocks.size(); i++) {
         const auto &Bk = c->blocks[i];
         const float *md = c->mod + i * 6 * (size_t) H;
-        // attention branch
-        if (!c->hip_ok(launch_fmt_ln_mod(c->x, md, ms, 0, H, R, H, g.ln_eps, c->h_a, Bk.qkv.f16, st), "norm") ||
-            !linear(c, Bk.qkv, c->h_a, R, c->qkv, nullptr, false, 0) ||
+        const bool last = i + 1 == c->blocks.size();
+        // attention branch, then the MLP branch's norm
+        if (!linear(c, Bk.qkv, c->h_a, R, c->qkv, nullptr, false, 0) ||
             !c->hip_ok(launch_fmt_attn(c->qkv, c->B, T, H, g.n_heads, g.attn_window, c->o_a, Bk.proj.f16, st),
                        "attention") ||
-            !linear(c, Bk.proj, c->o_a, R, c->x, nullptr, false, 0, md + 2 * H, ms, c->x))
+            !residual_norm(Bk.proj, c->o_a, md + 2 * H, md, 3 * H, 4 * H, Bk.fc1.f16))
             return false;
-        // MLP branch
-        if (!c->hip_ok(launch_fmt_ln_mod(c->x, md, ms, 3 * H, 4 * H, R, H, g.ln_eps, c->h_a, Bk.fc1.f16, st),
-                       "norm") ||
-            !linear(c, Bk.fc1, c->h_a, R, nullptr, c->m1_a, Bk.fc2.f16, 2) ||
-            !linear(c, Bk.fc2, c->m1_a, R, c->x, nullptr, false, 0, md + 5 * H, ms, c->x))
+        // MLP branch, then the next block's attention norm (the final layer's norm after the last)
+        const float *nmd = last ? fmd : md + 6 * (size_t) H;
+        const bool n16 = last ? c->fin_lin.f16 : c->blocks[i + 1].qkv.f16;
+        if (!linear(c, Bk.fc1, c->h_a, R, nullptr, c->m1_a, Bk.fc2.f16, 2) ||
+            !residual_norm(Bk.fc2, c->m1_a, md + 5 * H, nmd, 0, H, n16))
             return false;
     }
-    // final head
-    const float *fmd = c->mod + c->blocks.size() * 6 * (size_t) H;
-    if (!c->hip_ok(launch_fmt_ln_mod(c->x, fmd, ms, 0, H, R, H, g.ln_eps, c->h_a, c->fin_lin.f16, st),
-                   "norm") ||
-        !linear(c, c->fin_lin, c->h_a, R, c->v, nullptr, false, 0))
+    // final head (its norm came with the last block's residual update)
+    if (c->blocks.empty() &&
+        !c->hip_ok(launch_fmt_ln_mod(c->x, fmd, ms, 0, H, R, H, g.ln_eps, c->h_a, c->fin_lin.f16, st), "norm"))
         return false;
+    if (!linear(c, c->fin_lin, c->h_a, R, c->v, nullptr, false, 0)) return false;
     return true;
 }
 
