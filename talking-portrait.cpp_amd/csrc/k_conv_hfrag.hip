@@ -15,6 +15,9 @@ static int hfrag_config(bool f16, int mode, int IC, int H, int W, int M) {
         if (M % bm != 0 || H % th != 0 || W % tw != 0) return 0;
         return (int64_t) (M / bm) * 16 * (H / th) * (W / tw);
     };
+    // the 128-channel up-conv (r256): 128-row tiles on four waves, two
+    // workgroups per CU
+    if (IC == 128 && mode == MODE_SUBPIX && tiles(128, 8, 32) >= 256) return 2;
     if (tiles(256, 8, 32) >= 256) return 1;
     if (tiles(128, 8, 32) >= 256) return 2;
     if (tiles(128, 16, 16) >= 256) return 3;

@@ -31,11 +31,16 @@ namespace tpmd {
 //   * the halo of chunk c+1 is loaded into registers early in chunk c and
 //     written to the other LDS buffer late in it; one barrier ends the chunk.
 // Configurations (hfrag_config):
-//   * 256 rows x 8 x 32 pixels (the r64 - r256 up-convs): eight waves of
+//   * 256 rows x 8 x 32 pixels (the r64 and r128 up-convs): eight waves of
 //     64 x 128 (two per SIMD), and for IC = 512 (the r64 up-conv) four waves
 //     of 128 x 128 (one per SIMD, 16 MFMAs per 4 A and 4 B fragments: half
 //     the A requests per MFMA; 137 -> 132 us per 16-frame launch in the
-//     decoder; the r128 and r256 up-convs measured the same either way);
+//     decoder; the r128 up-conv measured the same either way);
+//   * 128 rows x 8 x 32 pixels on four waves of 64 x 128 for IC = 128 (the
+//     r256 up-conv): at most 256 registers and 68 KB of LDS, so two
+//     workgroups share a CU and one's prologue and store epilogue run under
+//     the other's MFMAs (155.3 -> 150.8 us per 16-frame launch against the
+//     one-per-CU 256-row form);
 //   * 128 rows x 8 x 32 or x 16 x 16 pixels where 256 rows leave fewer than
 //     256 tiles at 16 frames (the r32 convs: a 32 x 32 map, a 16 x 16 up-conv
 //     input): eight waves of 64 x 64, and for IC = 512 four waves of 64 x 128:
@@ -59,8 +64,11 @@ struct hfrag_cfg {
     static_assert(HPX * HR_PXB <= HR_HBUF, "halo buffer");
 };
 
-template <int MODE, int NC, int BM, int TH, int TW, typename TO, int NW_ = 8, int TM_ = 2>
-__global__ __launch_bounds__(NW_ * 64) void modconv3x3_hfrag_kernel(ConvParams p, int tiles_x, int tiles_frame) {
+// WPE: waves per SIMD the registers must allow (2: at most 256 registers, so
+// two four-wave workgroups share a CU)
+template <int MODE, int NC, int BM, int TH, int TW, typename TO, int NW_ = 8, int TM_ = 2, int WPE = 1>
+__global__ __launch_bounds__(NW_ * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void modconv3x3_hfrag_kernel(
+    ConvParams p, int tiles_x, int tiles_frame) {
     typedef half_t TA;
     typedef hfrag_cfg<BM, TH, TW, NW_, TM_> F;
     constexpr int NW = F::NW, NT = F::NT, WN = F::WN, BN = F::BN, TM = F::TM, TN = F::TN;
@@ -273,6 +281,13 @@ hipError_t launch_hfrag_nc(const ConvParams &p, int cfg, int mode, bool out_f16,
         if constexpr (NC == 16 && B == 256) {
             if (mode == MODE_SUBPIX) {
                 hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC, B, T_H, T_W, half_t, 4, 4>), grid,
+                                   dim3(256), 0, st, p, tiles_x, tiles_frame);
+                return hipGetLastError();
+            }
+        }
+        if constexpr (NC == 4 && B == 128 && T_H == 8) {
+            if (mode == MODE_SUBPIX) {
+                hipLaunchKernelGGL((modconv3x3_hfrag_kernel<MODE_SUBPIX, NC, B, T_H, T_W, half_t, 4, 2, 2>), grid,
                                    dim3(256), 0, st, p, tiles_x, tiles_frame);
                 return hipGetLastError();
             }
