@@ -213,7 +213,8 @@ struct tpmd_ctx {
     // per-batch buffers of one launch chain.  Device-resident decodes on the
     // library's own stream rotate over kLanes lanes, each with its own
     // buffers and stream, so consecutive batches overlap on the GPU
-    // (measured at 16 frames: 2 lanes 9.9k frames/s, 3 lanes 10.05k, 4 lanes 9.8k)
+    // (measured at 16 frames: 2 lanes 9.9k frames/s, 3 lanes 10.05k, 4 lanes 9.8k;
+    // with later kernels 3 lanes 12.36k, 4 lanes 11.98k, 5 lanes 11.77k)
     static constexpr int kLanes = 3;
     struct Lane {
         float *lat = nullptr, *s_all = nullptr, *den_all = nullptr;
