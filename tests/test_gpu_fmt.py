@@ -64,6 +64,23 @@ def test_fmt_sample_chunk(oracle_fmt, torch_cuda, ftype):
         _close(ftype, fm.sample_chunk(*args), ref.sample_chunk(*args), ("chunk", emo))
 
 
+def test_fmt_own_gemm_f16(oracle_fmt, torch_cuda, monkeypatch):
+    """f16 weights with TPFM_BLASLT=0 at prepare: every linear on the
+    library's own split-K GEMM and epilogue pass instead of hipBLASLt, the
+    residual updates in the epilogue pass and the norms on their own; same
+    tolerances against the oracle, forward (reference dims) and chunk"""
+    monkeypatch.setenv("TPFM_BLASLT", "0")
+    ocfg, _, ref, fm = _pair(oracle_fmt, "f16", {})
+    io = synth.fmt_chunk_inputs(ocfg)
+    cond = ref.cond_rows(io["wr"], io["prev_wa"], io["cond_audio"], 2)
+    x60 = np.concatenate([io["prev_x"], io["x0"]])
+    _close("f16", fm.forward(x60, cond, 0.3), ref.forward(x60, cond, 0.3), "forward")
+    ocfg2, _, ref2, fm2 = _pair(oracle_fmt, "f16", _small(oracle_fmt))
+    io2 = synth.fmt_chunk_inputs(ocfg2)
+    args = (io2["wr"], io2["prev_x"], io2["prev_wa"], io2["cond_audio"], 3, io2["x0"])
+    _close("f16", fm2.sample_chunk(*args), ref2.sample_chunk(*args), ("chunk", 3))
+
+
 def test_fmt_gguf(oracle_fmt, torch_cuda, tmp_path):
     """tpfm_read_config + tpfm_load_gguf on a float-fmt file == named weights"""
     kw = _small(oracle_fmt)
